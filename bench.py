@@ -1,0 +1,223 @@
+"""moe_block benchmark on one MI355X.
+
+Default workload: config c1 (OLMoE shape, int4-g64, D=2048, I=1024, 64 experts,
+top-8, SwiGLU) at T=16 decode tokens.  One step = one mvllm_hip_moe_block_dev call
+(gate/up/act GEMV, down GEMV, top-k combine) with weights, activations and output
+already resident in HBM.  Every step reads its experts from a different layer of a
+>= 4 GiB weight pool, so the 256 MB Infinity Cache cannot serve repeated weights.
+
+Prints ONE JSON line on stdout; details go to stderr.
+  python bench.py [--steps K] [--warmup W] [--config c1] [--tokens T] [--mode M]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "micro-vllm_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+
+HBM_PEAK_GBS = 8000.0
+FP4_PEAK_TFS = 10100.0
+BF16_PEAK_TFS = 2500.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_pool(torch, mvllm_hip, fmt, D, I, n_blobs, seed):
+    """n_blobs expert blobs in the reference layout, generated on the GPU."""
+    nbytes, off = mvllm_hip.expert_geom(fmt, D, I)
+    stride = (nbytes + 255) // 256 * 256
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pool = torch.randint(0, 256, (n_blobs, stride), dtype=torch.uint8, device="cuda",
+                         generator=g)
+    gq = 64 if fmt == 4 else 32
+    pieces = [(1, I, D), (3, I, D), (5, D, I)]  # scale pieces: (offset index, rows O, K)
+    for oi, O, K in pieces:
+        ns = O * ((K + gq - 1) // gq)
+        o = int(off[oi])
+        if fmt == 4:
+            s = torch.empty((n_blobs, ns), dtype=torch.float32, device="cuda")
+            s.uniform_(0.005, 0.02, generator=g)
+            s = s.to(torch.bfloat16).to(torch.float32)  # bf16-valued scales stored as f32
+            pool[:, o:o + 4 * ns] = s.view(torch.uint8).view(n_blobs, 4 * ns)
+        else:
+            pool[:, o:o + ns] = torch.randint(118, 125, (n_blobs, ns), dtype=torch.uint8,
+                                              device="cuda", generator=g)
+    return pool, stride, off, nbytes
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", default="c1")
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--mode", type=int, default=0)
+    ap.add_argument("--pool-gb", type=float, default=4.5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the expert-parallel sharding is a design note); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import mvllm_hip
+    from mvllm_hip import synth
+
+    cfg = dict(synth.CONFIGS[args.config])
+    T = args.tokens or cfg["T"]
+    D, I, E, k, fmt = cfg["D"], cfg["I"], cfg["E"], cfg["k"], cfg["fmt"]
+    mvllm_hip.init(0)
+    mvllm_hip.set_option("mode", args.mode)
+
+    w = synth.make_workload(args.config, T=T, with_experts=False)
+    nbytes, _ = mvllm_hip.expert_geom(fmt, D, I)
+    layers = max(1, int(np.ceil(args.pool_gb * 2**30 / (nbytes * w.nb))))
+    n_blobs = layers * w.nb
+    log(f"workload {args.config} T={T}: {w.nb} experts, {int(w.nr.sum())} rows, "
+        f"{layers} pool layers x {w.nb} blobs of {nbytes/2**20:.2f} MiB "
+        f"({n_blobs * nbytes / 2**30:.2f} GiB)")
+    pool, stride, off, _ = build_pool(torch, mvllm_hip, fmt, D, I, n_blobs, 1234)
+    base = pool.data_ptr()
+
+    def lists(layer):
+        ptrs = [[], [], [], [], [], []]  # g, u, d, gs, us, ds
+        order = (0, 2, 4, 1, 3, 5)       # geometry offsets: gate_p gate_s up_p up_s down_p down_s
+        for i in range(w.nb):
+            b = base + (layer * w.nb + i) * stride
+            for slot, oi in enumerate(order):
+                ptrs[slot].append(b + int(off[oi]))
+        return ptrs
+
+    layer_lists = [lists(l) for l in range(layers)]
+    xg = torch.from_numpy(w.xg).cuda()
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+
+    def step(s):
+        g, u, d, gs, us, ds = layer_lists[s % layers]
+        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, g, u, d, gs, us, ds, xg, w.xoff, w.nr, w.rows,
+                                w.rw, out, T, w.act, w.a, w.b)
+
+    for s in range(args.warmup):
+        step(s)
+    torch.cuda.synchronize()
+
+    # timed region: K steps bracketed by synchronize; per-kernel HIP events are recorded
+    # by the library on the same stream
+    mvllm_hip.set_option("timing", 1)
+    mvllm_hip.stats_reset()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for s in range(args.steps):
+        step(s)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    st = mvllm_hip.stats()
+    mvllm_hip.set_option("timing", 0)
+    ms_gu = st["ms_gate_up"] / args.steps
+    ms_dn = st["ms_down"] / args.steps
+    ms_cb = st["ms_combine"] / args.steps
+
+    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+    b_gu = 2 * (I * (D // 2) + I * ((D + gq - 1) // gq) * sb)   # gate + up, one expert
+    b_dn = D * (I // 2) + D * ((I + gq - 1) // gq) * sb          # down, one expert
+    wbytes = w.nb * (b_gu + b_dn)
+    flops = 6.0 * D * I * float(w.nr.sum())
+    tok_s = T / (ms_step * 1e-3)
+    log(f"step {ms_step*1e3:.1f} us (wall {wall/args.steps*1e6:.1f} us): gate/up "
+        f"{ms_gu*1e3:.1f} us, down {ms_dn*1e3:.1f} us, combine {ms_cb*1e3:.1f} us; "
+        f"effective weight {wbytes/ms_step/1e6:.0f} GB/s")
+    gu_gbs = w.nb * b_gu / (ms_gu * 1e-3) / 1e9
+    dn_gbs = w.nb * b_dn / (ms_dn * 1e-3) / 1e9
+    log(f"gate/up {gu_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, args.cpu_seconds)
+
+    rec = {
+        "metric": "moe_block tokens/s (decode), effective weight GB/s",
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded; weights random in the reference layouts, in a "
+                f"{n_blobs * nbytes / 2**30:.1f} GiB pool rotated per step)",
+        "config": {"workload": f"{args.config} {cfg['desc']}, T={T}", "D": D, "I": I, "E": E,
+                   "topk": k, "T": T, "fmt": fmt, "experts_per_step": int(w.nb),
+                   "rows": int(w.nr.sum()), "mode": args.mode},
+        "weight_gbps": round(wbytes / ms_step / 1e6, 1),
+        "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "bytes_per_launch": int(w.nb * b_gu), "avg_launch_us": round(ms_gu * 1e3, 3)},
+        "phases_us": {"gate_up": round(ms_gu * 1e3, 3), "down": round(ms_dn * 1e3, 3),
+                      "combine": round(ms_cb * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):
+    """The reference's host moe_block (oracle/_ref build when present, else the C
+    restatement) on layer 0's experts, single thread, bounded to ~budget_s."""
+    import oracle
+    kind = "reference" if oracle.have_ref() else "port"
+    cpu = oracle.CpuMoe("ref" if kind == "reference" else "oracle")
+    host = pool[:w.nb].cpu().numpy()
+    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+
+    def piece(i, oi, O, K, scale):
+        o = int(off[oi])
+        if scale:
+            n = O * ((K + gq - 1) // gq)
+            a = host[i, o:o + n * sb]
+            return a.view(np.float32 if fmt == 4 else np.uint8).reshape(O, -1)
+        return host[i, o:o + O * ((K + 1) // 2)].reshape(O, -1)
+
+    g = [piece(i, 0, I, D, False) for i in range(w.nb)]
+    gs = [piece(i, 1, I, D, True) for i in range(w.nb)]
+    u = [piece(i, 2, I, D, False) for i in range(w.nb)]
+    us = [piece(i, 3, I, D, True) for i in range(w.nb)]
+    d = [piece(i, 4, D, I, False) for i in range(w.nb)]
+    ds = [piece(i, 5, D, I, True) for i in range(w.nb)]
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        o = np.zeros((T, D), np.float32)
+        cpu.moe_block(w.nb, D, I, fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, o,
+                      T, w.act, w.a, w.b)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or calls >= 50:
+            break
+    per = el / calls
+    log(f"cpu baseline ({kind}, 1 thread): {per*1e3:.1f} ms/call over {calls} calls")
+    return {"value": round(T / per, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
+            "sample": f"{calls} full moe_block calls of the same workload (T={T}, {w.nb} experts) "
+                      f"in {el:.1f} s, single-threaded host code",
+            "ms_per_call": round(per * 1e3, 3), "nproc": os.cpu_count()}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+/*
+ * mvllm_hip.h -- C ABI of the MI355X (gfx950) routed-expert moe_block backend.
+ *
+ * This is the drop-in boundary.  Every entry point takes plain pointers and sizes
+ * (no torch or C++ types) and names the reference interface it replaces.  The
+ * reference is micro-vllm; paths below are relative to its tree.
+ *
+ * Return convention (same as the reference's device ops, src/gpu/metal_ops.hpp:9-10):
+ * 1 = ran, 0 = "use the host kernel" (bad arguments, no device, or a HIP error;
+ * mvllm_hip_last_error() then says which).  No entry point throws.
+ *
+ * Weight formats (fmt), byte-identical to src/quant:
+ *   0  f32 row-major [O, K]                                  (src/quant/quant.cpp:156-168)
+ *   4  int4-g64: nibbles [O, (K+1)/2], low nibble = even k, value (n-8)*scale;
+ *      f32 scales [O, ceil(K/64)]                            (src/quant/quant.cpp:203-228)
+ *   7  MXFP4: e2m1 nibbles [O, (K+1)/2]; ue8m0 scale bytes [O, ceil(K/32)], passed
+ *      through the const float* slots                        (src/quant/quant.cpp:298-321)
+ * For gate/up O = Iinter, K = D; for down O = D, K = Iinter.
+ */
+#ifndef MVLLM_HIP_H
+#define MVLLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- lifecycle: metal_ops::init / shutdown / available / backend_name
+ *      (src/gpu/metal_ops.hpp:15-18); device selection gpu::select
+ *      (src/gpu/backend.cpp:92-113) for Device::Hip. ------------------------- */
+
+/* Selects HIP device `device` and creates the backend's streams.  1 ok, 0 no device. */
+int mvllm_hip_init(int device);
+/* Waits for outstanding work, frees device memory the backend owns. */
+void mvllm_hip_shutdown(void);
+/* 1 after a successful init. */
+int mvllm_hip_available(void);
+/* "hip" -- the string the engine's info tag shows as coli=hip
+ * (src/model/glm53.cpp:407-413, src/model/kimi_k3.cpp:740-746). */
+const char *mvllm_hip_name(void);
+/* Text of the last failure on this thread's most recent call ("" if none). */
+const char *mvllm_hip_last_error(void);
+
+/* ---- the hot path ---------------------------------------------------------- */
+
+/* Drop-in for metal_ops::moe_block (src/gpu/metal_ops.hpp:99-108,
+ * src/gpu/metal_ops.cpp:448-460).  All pointers are caller-owned HOST memory,
+ * exactly as in the reference: per expert e, nr[e] rows of xg starting at row
+ * xoff[e] go through gate/up -> act -> down, and out[rows[j]] += rw[j] * y[j]
+ * in expert order.  act: 0 Silu, 1 ClampSwiGLU(act_a), 2 SiTU(act_a, act_b).
+ * Validation and skip rules are the reference's (nb<1, D<1, !out, !xg, fmt not in
+ * {0,4,7}, !xoff, !nr -> 0; null expert pointers or Iinter<1 consume rows without
+ * writing; rows outside [0,S) (S>0) are skipped).  Expert weights that were
+ * promoted with mvllm_hip_promote are read from HBM; others are copied in.
+ * Synchronous: out holds the result on return. */
+int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                        const void *const *u, const void *const *d, const float *const *gs,
+                        const float *const *us, const float *const *ds, const float *xg,
+                        const int *xoff, const int *nr, const int *rows, const float *rw,
+                        float *out, int S, int act, float act_a, float act_b);
+
+/* Same contract for GPU-resident callers (no reference counterpart beyond
+ * moe_block itself, src/gpu/metal_ops.hpp:104-108): the six pointer arrays and
+ * xoff/nr/rows/rw are HOST arrays; the weights and scales they point to, xg
+ * ([rows, D] f32) and out ([S, D] f32, accumulated) are DEVICE pointers.
+ * Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and the
+ * call returns without waiting.  Requires S > 0 (out's row count). */
+int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                            const void *const *u, const void *const *d,
+                            const float *const *gs, const float *const *us,
+                            const float *const *ds, const float *xg, const int *xoff,
+                            const int *nr, const int *rows, const float *rw, float *out, int S,
+                            int act, float act_a, float act_b, void *stream);
+
+/* Numerics mode for segments of many rows (prefill).  The decode GEMV (segments
+ * of <= mvllm_hip_set_option("mfma_min_rows") rows) always accumulates in f32.
+ *   0  auto: f32 GEMV for short segments, bf16 MFMA for long ones (default)
+ *   1  f32 everywhere (exact-order-independent f32 GEMV; slow for prefill)
+ *   2  bf16 MFMA for every segment of fmt 4 / 7
+ *   3  like 0, but fmt 7 long segments quantize activations to MXFP4
+ *      (fp4_activation_qdq semantics, src/quant/native_act.cpp:159-179) and run
+ *      the gfx950 scaled FP4 MFMA.
+ * Options (key, value): "mode" (above), "mfma_min_rows" (default 32),
+ * "timing" (1 = record per-kernel HIP events; read them with mvllm_hip_stats).
+ * Returns 1 if the key is known. */
+int mvllm_hip_set_option(const char *key, long long value);
+
+/* ---- segment construction: moe_union_ids (src/model/ops.cpp:1082-1099) and the
+ *      per-expert gather of moe_layer_n (src/model/glm53.cpp:1938-1971,
+ *      src/model/kimi_k3.cpp:2009-2050).  Host integer work, bit-exact. ------- */
+
+/* Sorted unique non-negative ids of idx[n_tok*topk], at most out_cap. */
+int mvllm_moe_union_ids(const int *idx, int n_tok, int topk, int *out, int out_cap);
+
+/* Arguments for ONE batched moe_block call that reproduces moe_layer_n's
+ * per-expert loop: eids[nb] ascending; expert i owns rows [xoff[i], xoff[i]+nr[i]);
+ * row j is token rows[j] (also its gather index into the token matrix) with weight
+ * rw[j] = sum of that token's top-k weights for the expert (rows whose sum is 0
+ * are dropped, as the reference does).  Returns nb, or -1 if a capacity is short;
+ * *n_rows receives the total row count. */
+int mvllm_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int *eids,
+                       int *xoff, int *nr, int *rows, float *rw, int cap_experts, int cap_rows,
+                       int *n_rows);
+
+/* Expert blob geometry (byte offsets of the six pieces inside one expert blob):
+ * fmt 4 = GLM gate_p|gate_s|up_p|up_s|down_p|down_s (src/model/glm53.cpp:56-78,
+ * 116-132); fmt 7 = K3 w1p|w1s|w2p|w2s|w3p|w3s with gate=w1, down=w2, up=w3
+ * (src/model/kimi_k3.cpp:83-102, 132-159).  off[6] = gate_p, gate_s, up_p, up_s,
+ * down_p, down_s.  Returns the blob size in bytes, or -1 for a bad fmt/shape. */
+long long mvllm_expert_geom(int fmt, int D, int Iinter, long long off[6]);
+
+/* ---- HBM expert residency (the LRU tier in front of ExpertStore,
+ *      src/store/expert_store.hpp:71-175).  Blobs are keyed by (layer, eid). -- */
+
+/* Page-locked host memory for ExpertStore slots (replaces aligned_alloc_pages,
+ * src/io/file_io.cpp:95, so promotion copies are truly asynchronous). */
+void *mvllm_hip_host_alloc(size_t bytes);
+void mvllm_hip_host_free(void *p);
+
+/* Sets the HBM budget of the expert tier (bytes; default 64 GiB). */
+int mvllm_hip_set_expert_budget(size_t bytes);
+
+/* Starts an asynchronous copy of one expert blob (host_blob, bytes) into HBM on
+ * the backend's copy stream, evicting least-recently-used blobs when the budget
+ * is full.  Later moe_block calls whose expert pointers fall inside
+ * [host_blob, host_blob+bytes) read the HBM copy once the copy's event has
+ * completed (the compute stream waits on it).  Already resident: only bumps LRU.
+ * 1 ok, 0 failure. */
+int mvllm_hip_promote(const void *host_blob, size_t bytes, int layer, int eid);
+
+/* Drops the HBM copy of (layer, eid); call it when ExpertStore reuses the slot
+ * (its REPIN / evict path, src/store/expert_store.cpp:350-405).  1 if found. */
+int mvllm_hip_evict(int layer, int eid);
+
+/* Device address of a resident blob (NULL if absent); waits for its copy. */
+void *mvllm_hip_resident_ptr(int layer, int eid);
+
+/* Counters since init (or the last reset): index
+ *  0 moe_block calls      1 rows computed        2 H2D bytes (weights)
+ *  3 H2D bytes (acts/out) 4 D2H bytes            5 promotions
+ *  6 resident hits        7 misses (copied in)   8 evictions
+ *  9 kernel ms gate/up    10 kernel ms down      11 kernel ms combine
+ *  12 kernel ms quantize  13 launches gate/up    14 launches down
+ * Kernel times are filled only with option "timing"=1.  Returns the count
+ * written (<= n). */
+int mvllm_hip_stats(double *vals, int n);
+void mvllm_hip_stats_reset(void);
+
+/* ---- checking aids (no reference counterpart: they expose the device's view
+ *      of the quantized formats so tests can pin it bit for bit) ------------ */
+
+/* Dequantizes one device matrix to f32 [O, K] on the device exactly as the
+ * kernels see it: fmt 4 (n-8)*scale, fmt 7 lut[n]*2^(e-127) with e=0 -> +0 and
+ * e=255 -> +inf (src/quant/quant.hpp:13-20).  Synchronous.  1 ok. */
+int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, int O, int K,
+                      float *w_dev);
+
+/* MXFP4 activation quantization on the device, bit-exact with fp4_activation_qdq
+ * (src/quant/native_act.cpp:159-179) for block 32: rows x [n, K] f32 ->
+ * codes [n, K/2] packed e2m1 (low nibble = even k) + scales [n, K/32] ue8m0.
+ * K must be a multiple of 32.  Synchronous.  1 ok. */
+int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
+                             uint8_t *scales_dev);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MVLLM_HIP_H */

@@ -1,0 +1,117 @@
+// kern_misc.hip -- top-k combine and MXFP4 activation quantization for gfx950.
+#include "moe_internal.h"
+
+#include <cmath>
+
+namespace mvllm_hip {
+
+// out[t] += w_e * Y[e] for the token's entries in reference order (expert order, then
+// row order), each step rounded as `orow[i] += w * hr[i]` rounds on the host
+// (src/gpu/metal_ops.cpp:328-339): a product, then a sum, no fused multiply-add.
+__global__ __launch_bounds__(256) void k_combine(CombineArgs A) {
+    const int t = blockIdx.y;
+    const int e0 = A.tok_ptr[t], e1 = A.tok_ptr[t + 1];
+    float *orow = A.out + (size_t)A.out_row[t] * (size_t)A.D;
+    if ((A.D & 3) == 0 && ((uintptr_t)A.out & 15) == 0) {
+        const int d4 = blockIdx.x * 256 + threadIdx.x;
+        if (d4 * 4 >= A.D)
+            return;
+        float4 o = reinterpret_cast<float4 *>(orow)[d4];
+        for (int e = e0; e < e1; ++e) {
+            const float w = A.ent_w[e];
+            const float4 y =
+                reinterpret_cast<const float4 *>(A.Y + (size_t)A.ent_row[e] * (size_t)A.D)[d4];
+            o.x = __fadd_rn(o.x, __fmul_rn(w, y.x));
+            o.y = __fadd_rn(o.y, __fmul_rn(w, y.y));
+            o.z = __fadd_rn(o.z, __fmul_rn(w, y.z));
+            o.w = __fadd_rn(o.w, __fmul_rn(w, y.w));
+        }
+        reinterpret_cast<float4 *>(orow)[d4] = o;
+    } else {
+        for (int d = blockIdx.x * 1024 + threadIdx.x; d < A.D && d < (blockIdx.x + 1) * 1024;
+             d += 256) {
+            float o = orow[d];
+            for (int e = e0; e < e1; ++e)
+                o = __fadd_rn(o, __fmul_rn(A.ent_w[e], A.Y[(size_t)A.ent_row[e] * A.D + d]));
+            orow[d] = o;
+        }
+    }
+}
+
+hipError_t launch_combine(const CombineArgs &a, hipStream_t st) {
+    if (a.n_tok <= 0)
+        return hipSuccess;
+    const dim3 grid((unsigned)((a.D + 1023) / 1024), (unsigned)a.n_tok), block(256);
+    hipLaunchKernelGGL(k_combine, grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+// ---- MXFP4 activation quantization (src/quant/native_act.cpp:159-179, block 32) ----
+
+// e2m1 magnitudes in code order 0..7
+__device__ __forceinline__ float e2m1_mag(int c) {
+    const int e = (c >> 1) & 3, m = c & 1;
+    return e == 0 ? 0.5f * (float)m : (1.f + 0.5f * (float)m) * (float)(1 << (e - 1));
+}
+
+// Nearest code with the reference's scan order 0..15 and strict '<' (lowest index wins
+// ties).  Codes 8..15 are the negatives and code 8 decodes to +0 there.
+__device__ __forceinline__ int nearest_e2m1(float v) {
+    int best = 0;
+    float dist = fabsf(v);
+    for (int c = 1; c < 16; ++c) {
+        const float val = c == 8 ? 0.f : (c & 8 ? -e2m1_mag(c & 7) : e2m1_mag(c));
+        const float d = fabsf(v - val);
+        if (d < dist) {
+            dist = d;
+            best = c;
+        }
+    }
+    return best;
+}
+
+// ceil(log2(v)) for a normal v > 0 (frexp exponent, minus one at exact powers of two)
+__device__ __forceinline__ int ceil_log2_normal(float v) {
+    const uint32_t b = __float_as_uint(v);
+    const int ef = (int)((b >> 23) & 0xffu);
+    return (b & 0x7fffffu) == 0 ? ef - 127 : ef - 126;
+}
+
+// one thread per 32-element block
+__global__ void k_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales) {
+    const int nb = K / 32;
+    const size_t total = (size_t)n * nb;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t row = i / nb, blk = i % nb;
+        const float *xb = x + row * (size_t)K + blk * 32;
+        float amax = 0.f;
+        for (int k = 0; k < 32; ++k) {
+            const float a = fabsf(xb[k]);
+            if (a > amax)
+                amax = a;
+        }
+        amax = fmaxf(amax, 6.f * 1.1754943508222875e-38f);  // 6 * 2^-126
+        int ex = ceil_log2_normal(amax / 6.f);
+        ex = ex < -127 ? -127 : (ex > 127 ? 127 : ex);
+        const uint32_t sc = (uint32_t)(ex + 127);
+        scales[i] = (uint8_t)sc;
+        const float scale = ldexpf(1.f, ex);
+        uint8_t *cb = codes + row * (size_t)(K / 2) + blk * 16;
+        for (int k = 0; k < 32; k += 2) {
+            const float q0 = fmaxf(-6.f, fminf(6.f, xb[k] / scale));
+            const float q1 = fmaxf(-6.f, fminf(6.f, xb[k + 1] / scale));
+            cb[k >> 1] = (uint8_t)(nearest_e2m1(q0) | (nearest_e2m1(q1) << 4));
+        }
+    }
+}
+
+hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
+                                 hipStream_t st) {
+    if (n <= 0 || K <= 0 || K % 32)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_quantize_mxfp4, dim3(1024), dim3(256), 0, st, x, n, K, codes, scales);
+    return hipGetLastError();
+}
+
+}  // namespace mvllm_hip

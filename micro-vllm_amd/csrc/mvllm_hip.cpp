@@ -1,0 +1,945 @@
+// mvllm_hip.cpp -- C ABI of the MI355X routed-expert moe_block backend (host side).
+//
+// Per call: validate exactly as metal_ops::moe_block does (src/gpu/metal_ops.cpp:448-460),
+// walk the experts with cpu_moe_block's skip rules (src/gpu/metal_ops.cpp:283-297) to
+// build a plan -- active experts, their compact rows (rows whose destination reaches
+// `out`), and per destination token the ordered list of (row, weight) it receives --
+// then run three stream-ordered phases: gate/up/act GEMV -> H, down GEMV -> Y, combine
+// Y into out in the reference's expert order.
+#include "../../include/mvllm_hip.h"
+#include "moe_internal.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <list>
+#include <map>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+using namespace mvllm_hip;
+
+namespace {
+
+thread_local std::string g_err;
+
+void set_err(const std::string &s) { g_err = s; }
+
+#define HIP_TRY(expr)                                                                         \
+    do {                                                                                      \
+        hipError_t e_ = (expr);                                                               \
+        if (e_ != hipSuccess) {                                                               \
+            set_err(std::string(#expr) + ": " + hipGetErrorString(e_));                       \
+            return 0;                                                                         \
+        }                                                                                     \
+    } while (0)
+
+// grow-only device buffer; growing waits for the device so no in-flight kernel reads it
+struct DevBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap)
+            return hipSuccess;
+        size_t want = std::max(bytes, cap + cap / 2);
+        want = (want + 255) & ~size_t(255);
+        if (p) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess)
+                return e;
+            (void)hipFree(p);
+            p = nullptr;
+            cap = 0;
+        }
+        hipError_t e = hipMalloc(&p, want);
+        if (e == hipSuccess)
+            cap = want;
+        return e;
+    }
+    void release() {
+        if (p)
+            (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+// grow-only pinned host buffer
+struct HostBuf {
+    void *p = nullptr;
+    size_t cap = 0;
+    hipError_t ensure(size_t bytes) {
+        if (bytes <= cap)
+            return hipSuccess;
+        size_t want = std::max(bytes, cap + cap / 2);
+        if (p)
+            (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+        hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+        if (e == hipSuccess)
+            cap = want;
+        return e;
+    }
+    void release() {
+        if (p)
+            (void)hipHostFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+};
+
+// One plan slot: pinned staging of the plan, its device copy, and an event that marks
+// the end of the call that last used the slot.
+struct PlanSlot {
+    HostBuf host;
+    DevBuf dev;
+    hipEvent_t done = nullptr;
+    bool used = false;
+};
+
+struct Resident {
+    int layer = 0, eid = 0;
+    const uint8_t *host = nullptr;
+    size_t bytes = 0;
+    void *dev = nullptr;
+    hipEvent_t ready = nullptr;    // copy finished (copy stream)
+    hipEvent_t last_use = nullptr; // last compute that read it
+    bool used = false;
+    std::list<long long>::iterator lru;
+};
+
+struct TimedCall {
+    hipEvent_t ev[4];  // start, after gate/up, after down, after combine
+};
+
+struct Ctx {
+    std::mutex mu;
+    bool ready = false;
+    int device = -1;
+    hipStream_t own = nullptr;   // compute stream for the host-pointer entry
+    hipStream_t copy = nullptr;  // promotions / misses
+    hipStream_t last_stream = nullptr;
+    hipEvent_t last_done = nullptr;  // end of the previous call (any stream)
+    bool have_last = false;
+    DevBuf H, Y, Xc, Oc, miss;
+    HostBuf hx, ho;
+    static constexpr int kSlots = 8;
+    PlanSlot slots[kSlots];
+    int slot_next = 0;
+    // options
+    int mode = 0;
+    int mfma_min_rows = 32;
+    int timing = 0;
+    // residency
+    size_t budget = size_t(64) << 30;
+    size_t used_bytes = 0;
+    std::unordered_map<long long, Resident> res;  // key = (layer << 32) | eid
+    std::map<const uint8_t *, long long> by_host;  // host blob start -> key
+    std::list<long long> lru;                      // front = most recent
+    std::multimap<size_t, void *> free_blocks;     // recycled device blocks by size
+    std::vector<std::pair<size_t, void *>> pending_free;
+    // stats
+    double stats[15] = {0};
+    std::vector<TimedCall> timed;
+};
+
+Ctx &ctx() {
+    static Ctx c;
+    return c;
+}
+
+long long res_key(int layer, int eid) {
+    return (static_cast<long long>(layer) << 32) | static_cast<unsigned>(eid);
+}
+
+// ---- plan -------------------------------------------------------------------------
+
+struct Plan {
+    std::vector<ExpertWork> ew;     // active experts
+    std::vector<int> src_expert;    // ew index -> caller's expert index e
+    std::vector<int> xrow;          // compact row -> row of xg
+    std::vector<int> dest;          // compact row -> destination row of out
+    std::vector<float> w;           // compact row -> combine weight
+    std::vector<int> tok_ptr, ent_row, out_row;
+    std::vector<float> ent_w;
+    int nr_max = 0;
+};
+
+size_t piece_bytes(int fmt, int piece, int D, int I) {
+    // piece: 0 gate/up packed, 1 gate/up scales, 2 down packed, 3 down scales
+    const size_t O = piece < 2 ? (size_t)I : (size_t)D;
+    const size_t K = piece < 2 ? (size_t)D : (size_t)I;
+    if (fmt == 0)
+        return (piece & 1) ? 0 : O * K * 4;
+    if (piece & 1)
+        return fmt == 4 ? O * ((K + 63) / 64) * 4 : O * ((K + 31) / 32);
+    return O * ((K + 1) / 2);
+}
+
+// Reference skip rules and row filtering (src/gpu/metal_ops.cpp:283-339).
+void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *g,
+                const void *const *u, const void *const *d, const float *const *gs,
+                const float *const *us, const float *const *ds, const int *xoff, const int *nr,
+                const int *rows, const float *rw, int S) {
+    P = Plan();
+    int base = 0;
+    for (int e = 0; e < nb; ++e) {
+        const int nre = nr[e];
+        if (nre <= 0)
+            continue;
+        bool ok = Iinter >= 1 && g && u && d && g[e] && u[e] && d[e];
+        if (ok && (fmt == 4 || fmt == 7))
+            ok = gs && us && ds && gs[e] && us[e] && ds[e];
+        if (ok && rows && rw) {
+            ExpertWork w{};
+            w.w[0] = g[e];
+            w.w[1] = u[e];
+            w.w[2] = d[e];
+            if (fmt != 0) {
+                w.s[0] = gs[e];
+                w.s[1] = us[e];
+                w.s[2] = ds[e];
+            }
+            w.row0 = static_cast<int>(P.xrow.size());
+            for (int r = 0; r < nre; ++r) {
+                const int dst = rows[base + r];
+                if (dst < 0 || (S > 0 && dst >= S))
+                    continue;
+                P.xrow.push_back(xoff[e] + r);
+                P.dest.push_back(dst);
+                P.w.push_back(rw[base + r]);
+            }
+            w.nrows = static_cast<int>(P.xrow.size()) - w.row0;
+            if (w.nrows > 0) {
+                P.ew.push_back(w);
+                P.src_expert.push_back(e);
+                P.nr_max = std::max(P.nr_max, w.nrows);
+            }
+        }
+        base += nre;
+    }
+    // combine CSR over destination tokens (ascending), entries in compact-row order
+    const int R = static_cast<int>(P.dest.size());
+    std::vector<int> order(R);
+    for (int j = 0; j < R; ++j)
+        order[j] = j;
+    std::stable_sort(order.begin(), order.end(),
+                     [&](int a, int b) { return P.dest[a] < P.dest[b]; });
+    for (int i = 0; i < R; ++i) {
+        const int j = order[i];
+        if (i == 0 || P.dest[j] != P.dest[order[i - 1]]) {
+            P.tok_ptr.push_back(i);
+            P.out_row.push_back(P.dest[j]);
+        }
+        P.ent_row.push_back(j);
+        P.ent_w.push_back(P.w[j]);
+    }
+    P.tok_ptr.push_back(R);
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// lanes per output row: the divisor of the chunk count closest to 4 chunks per lane
+int pick_lanes(int nch) {
+    int best = 64;
+    int bestd = 1 << 30;
+    for (int L : {64, 32, 16, 8}) {
+        if (nch % L)
+            continue;
+        const int dd = std::abs(nch / L - 4);
+        if (dd < bestd) {
+            bestd = dd;
+            best = L;
+        }
+    }
+    return best;
+}
+
+struct PhaseCfg {
+    bool fast;
+    int nr_max, L, passes, rows_per_tile, tiles;
+};
+
+PhaseCfg pick_phase(int fmt, int K, int O, const Plan &P, size_t first, size_t count,
+                    bool dual, const void *in) {
+    PhaseCfg c{};
+    c.fast = (fmt == 4 || fmt == 7) && K % 32 == 0 && aligned(in, 16);
+    for (size_t i = first; c.fast && i < first + count; ++i) {
+        const ExpertWork &w = P.ew[i];
+        for (int m = dual ? 0 : 2; m < (dual ? 2 : 3); ++m)
+            c.fast = c.fast && aligned(w.w[m], 16) && (fmt == 7 || aligned(w.s[m], 4));
+    }
+    int nrm = 0;
+    for (size_t i = first; i < first + count; ++i)
+        nrm = std::max(nrm, P.ew[i].nrows);
+    c.nr_max = nrm <= 1 ? 1 : nrm <= 2 ? 2 : nrm <= 4 ? 4 : 8;
+    if (c.fast) {
+        const int ks = gemv_kslice(c.nr_max, K);
+        c.L = pick_lanes(ks / 32);
+        c.passes = 1;
+        c.rows_per_tile = gemv_rows_per_tile(c.L, 1);
+        // keep very large grids within ~16K workgroups
+        while ((size_t)count * ((O + c.rows_per_tile - 1) / c.rows_per_tile) > 16384 &&
+               c.passes < 8) {
+            c.passes *= 2;
+            c.rows_per_tile = gemv_rows_per_tile(c.L, c.passes);
+        }
+    } else {
+        c.rows_per_tile = 4;
+    }
+    c.tiles = (O + c.rows_per_tile - 1) / c.rows_per_tile;
+    return c;
+}
+
+hipError_t run_gemv(int fmt, bool dual, const PhaseCfg &c, GemvArgs a, hipStream_t st) {
+    a.tiles_per_expert = c.tiles;
+    a.rows_per_tile = c.rows_per_tile;
+    return c.fast ? launch_gemv_fast(fmt, dual, c.nr_max, c.L, c.passes, a, st)
+                  : launch_gemv_generic(fmt, dual, a, st);
+}
+
+// Upload the plan (experts, xrow, combine CSR) through a pinned slot; returns device
+// pointers into the slot's device buffer.
+struct DevPlan {
+    ExpertWork *ew;
+    int *xrow, *tok_ptr, *ent_row, *out_row;
+    float *ent_w;
+    PlanSlot *slot;
+};
+
+int upload_plan(Ctx &C, const Plan &P, hipStream_t st, DevPlan &dp) {
+    PlanSlot &s = C.slots[C.slot_next];
+    C.slot_next = (C.slot_next + 1) % Ctx::kSlots;
+    if (s.used)
+        HIP_TRY(hipEventSynchronize(s.done));  // previous call on this slot is finished
+    auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
+    const size_t b_ew = al(P.ew.size() * sizeof(ExpertWork));
+    const size_t b_x = al(P.xrow.size() * 4), b_tp = al(P.tok_ptr.size() * 4);
+    const size_t b_er = al(P.ent_row.size() * 4), b_or = al(P.out_row.size() * 4);
+    const size_t b_ew2 = al(P.ent_w.size() * 4);
+    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2;
+    HIP_TRY(s.host.ensure(total));
+    HIP_TRY(s.dev.ensure(total));
+    char *h = static_cast<char *>(s.host.p);
+    size_t o = 0;
+    auto put = [&](const void *src, size_t n, size_t b) {
+        if (n)
+            std::memcpy(h + o, src, n);
+        const size_t at = o;
+        o += b;
+        return at;
+    };
+    const size_t o_ew = put(P.ew.data(), P.ew.size() * sizeof(ExpertWork), b_ew);
+    const size_t o_x = put(P.xrow.data(), P.xrow.size() * 4, b_x);
+    const size_t o_tp = put(P.tok_ptr.data(), P.tok_ptr.size() * 4, b_tp);
+    const size_t o_er = put(P.ent_row.data(), P.ent_row.size() * 4, b_er);
+    const size_t o_or = put(P.out_row.data(), P.out_row.size() * 4, b_or);
+    const size_t o_w = put(P.ent_w.data(), P.ent_w.size() * 4, b_ew2);
+    HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
+    char *d = static_cast<char *>(s.dev.p);
+    dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
+    dp.xrow = reinterpret_cast<int *>(d + o_x);
+    dp.tok_ptr = reinterpret_cast<int *>(d + o_tp);
+    dp.ent_row = reinterpret_cast<int *>(d + o_er);
+    dp.out_row = reinterpret_cast<int *>(d + o_or);
+    dp.ent_w = reinterpret_cast<float *>(d + o_w);
+    dp.slot = &s;
+    return 1;
+}
+
+// Scratch H/Y are shared by all calls: order this call after the previous one if it
+// came on another stream.
+int order_after_previous(Ctx &C, hipStream_t st) {
+    if (C.have_last && C.last_stream != st)
+        HIP_TRY(hipStreamWaitEvent(st, C.last_done, 0));
+    return 1;
+}
+
+int finish_call(Ctx &C, hipStream_t st, PlanSlot *slot) {
+    HIP_TRY(hipEventRecord(slot->done, st));
+    slot->used = true;
+    HIP_TRY(hipEventRecord(C.last_done, st));
+    C.last_stream = st;
+    C.have_last = true;
+    return 1;
+}
+
+// The three phases.  `split` experts [0, split) run gate/up first; a wait on
+// `gate_event` (may be null) precedes gate/up of [split, n).
+int run_phases(Ctx &C, const Plan &P, const DevPlan &dp, int fmt, int D, int I, int act,
+               float a, float b, const float *in, const int *in_rows, float *out,
+               hipStream_t st, size_t split, hipEvent_t gate_event) {
+    const size_t n = P.ew.size(), R = P.xrow.size();
+    HIP_TRY(C.H.ensure(std::max<size_t>(R * I * 4, 256)));
+    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
+    TimedCall tc{};
+    if (C.timing) {
+        for (auto &e : tc.ev)
+            HIP_TRY(hipEventCreate(&e));
+        HIP_TRY(hipEventRecord(tc.ev[0], st));
+    }
+    GemvArgs g{};
+    g.in_rows = in_rows;
+    g.in = in;
+    g.out = static_cast<float *>(C.H.p);
+    g.K = D;
+    g.O = I;
+    g.act = act;
+    g.act_a = a;
+    g.act_b = b;
+    for (int part = 0; part < 2; ++part) {
+        const size_t first = part == 0 ? 0 : split, cnt = part == 0 ? split : n - split;
+        if (part == 1 && gate_event)
+            HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+        if (!cnt)
+            continue;
+        g.ew = dp.ew + first;
+        g.n_experts = static_cast<int>(cnt);
+        const PhaseCfg c = pick_phase(fmt, D, I, P, first, cnt, true, in);
+        HIP_TRY(run_gemv(fmt, true, c, g, st));
+        C.stats[13] += 1;
+    }
+    if (C.timing)
+        HIP_TRY(hipEventRecord(tc.ev[1], st));
+    GemvArgs dn{};
+    dn.ew = dp.ew;
+    dn.n_experts = static_cast<int>(n);
+    dn.in_rows = nullptr;
+    dn.in = static_cast<const float *>(C.H.p);
+    dn.out = static_cast<float *>(C.Y.p);
+    dn.K = I;
+    dn.O = D;
+    {
+        const PhaseCfg c = pick_phase(fmt, I, D, P, 0, n, false, C.H.p);
+        HIP_TRY(run_gemv(fmt, false, c, dn, st));
+        C.stats[14] += 1;
+    }
+    if (C.timing)
+        HIP_TRY(hipEventRecord(tc.ev[2], st));
+    CombineArgs cb{};
+    cb.Y = static_cast<const float *>(C.Y.p);
+    cb.tok_ptr = dp.tok_ptr;
+    cb.ent_row = dp.ent_row;
+    cb.ent_w = dp.ent_w;
+    cb.out_row = dp.out_row;
+    cb.out = out;
+    cb.n_tok = static_cast<int>(P.out_row.size());
+    cb.D = D;
+    HIP_TRY(launch_combine(cb, st));
+    if (C.timing) {
+        HIP_TRY(hipEventRecord(tc.ev[3], st));
+        C.timed.push_back(tc);
+    }
+    C.stats[1] += static_cast<double>(R);
+    return 1;
+}
+
+bool args_ok(int nb, int D, int fmt, const float *xg, const int *xoff, const int *nr,
+             const float *out) {
+    // src/gpu/metal_ops.cpp:452-455
+    if (nb < 1 || D < 1 || !out || !xg || (fmt != 0 && fmt != 4 && fmt != 7)) {
+        set_err("invalid arguments (nb, D, out, xg or fmt)");
+        return false;
+    }
+    if (!xoff || !nr) {
+        set_err("xoff and nr are required");
+        return false;
+    }
+    return true;
+}
+
+// ---- residency --------------------------------------------------------------------
+
+void *res_alloc(Ctx &C, size_t bytes) {
+    auto it = C.free_blocks.find(bytes);
+    if (it != C.free_blocks.end()) {
+        void *p = it->second;
+        C.free_blocks.erase(it);
+        return p;
+    }
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess)
+        return nullptr;
+    return p;
+}
+
+void res_drop(Ctx &C, long long key) {
+    auto it = C.res.find(key);
+    if (it == C.res.end())
+        return;
+    Resident &r = it->second;
+    // the block is recycled only after readers and the copy are done: the copy
+    // stream waits for the last reader before writing into a recycled block
+    if (r.used)
+        (void)hipStreamWaitEvent(C.copy, r.last_use, 0);
+    C.free_blocks.emplace(r.bytes, r.dev);
+    C.used_bytes -= r.bytes;
+    C.by_host.erase(r.host);
+    C.lru.erase(r.lru);
+    (void)hipEventDestroy(r.ready);
+    (void)hipEventDestroy(r.last_use);
+    C.res.erase(it);
+    C.stats[8] += 1;
+}
+
+// device address for host pointer p (inside a resident blob), or nullptr
+Resident *res_lookup(Ctx &C, const void *p) {
+    const uint8_t *q = static_cast<const uint8_t *>(p);
+    auto it = C.by_host.upper_bound(q);
+    if (it == C.by_host.begin())
+        return nullptr;
+    --it;
+    Resident &r = C.res[it->second];
+    if (q >= r.host + r.bytes)
+        return nullptr;
+    return &r;
+}
+
+}  // namespace
+
+// ====================================================================================
+
+extern "C" {
+
+int mvllm_hip_init(int device) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (C.ready)
+        return C.device == device ? 1 : 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) {
+        set_err("no HIP device " + std::to_string(device));
+        return 0;
+    }
+    HIP_TRY(hipSetDevice(device));
+    HIP_TRY(hipStreamCreateWithFlags(&C.own, hipStreamNonBlocking));
+    HIP_TRY(hipStreamCreateWithFlags(&C.copy, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&C.last_done, hipEventDisableTiming));
+    for (auto &s : C.slots)
+        HIP_TRY(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+    C.device = device;
+    C.ready = true;
+    return 1;
+}
+
+void mvllm_hip_shutdown(void) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    if (!C.ready)
+        return;
+    (void)hipDeviceSynchronize();
+    while (!C.res.empty())
+        res_drop(C, C.res.begin()->first);
+    for (auto &fb : C.free_blocks)
+        (void)hipFree(fb.second);
+    C.free_blocks.clear();
+    C.H.release();
+    C.Y.release();
+    C.Xc.release();
+    C.Oc.release();
+    C.miss.release();
+    C.hx.release();
+    C.ho.release();
+    for (auto &s : C.slots) {
+        s.host.release();
+        s.dev.release();
+        (void)hipEventDestroy(s.done);
+        s.done = nullptr;
+        s.used = false;
+    }
+    for (auto &t : C.timed)
+        for (auto &e : t.ev)
+            (void)hipEventDestroy(e);
+    C.timed.clear();
+    (void)hipEventDestroy(C.last_done);
+    (void)hipStreamDestroy(C.own);
+    (void)hipStreamDestroy(C.copy);
+    C.have_last = false;
+    C.ready = false;
+    C.device = -1;
+}
+
+int mvllm_hip_available(void) { return ctx().ready ? 1 : 0; }
+
+const char *mvllm_hip_name(void) { return "hip"; }
+
+const char *mvllm_hip_last_error(void) { return g_err.c_str(); }
+
+int mvllm_hip_set_option(const char *key, long long value) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    if (!key)
+        return 0;
+    const std::string k(key);
+    if (k == "mode") {
+        if (value < 0 || value > 3)
+            return 0;
+        C.mode = static_cast<int>(value);
+    } else if (k == "mfma_min_rows") {
+        C.mfma_min_rows = static_cast<int>(std::max<long long>(1, value));
+    } else if (k == "timing") {
+        C.timing = value ? 1 : 0;
+    } else {
+        return 0;
+    }
+    return 1;
+}
+
+int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                            const void *const *u, const void *const *d, const float *const *gs,
+                            const float *const *us, const float *const *ds, const float *xg,
+                            const int *xoff, const int *nr, const int *rows, const float *rw,
+                            float *out, int S, int act, float act_a, float act_b,
+                            void *stream) {
+    (void)qgs;  // the reference ignores it too: 64 for fmt 4, 32 for fmt 7
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready) {
+        set_err("mvllm_hip_init not called");
+        return 0;
+    }
+    if (!args_ok(nb, D, fmt, xg, xoff, nr, out))
+        return 0;
+    if (S <= 0) {
+        set_err("the device entry needs S > 0 (row count of out)");
+        return 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    Plan P;
+    build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
+    C.stats[0] += 1;
+    if (P.ew.empty())
+        return 1;
+    if (!order_after_previous(C, st))
+        return 0;
+    DevPlan dp{};
+    if (!upload_plan(C, P, st, dp))
+        return 0;
+    if (!run_phases(C, P, dp, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
+                    P.ew.size(), nullptr))
+        return 0;
+    return finish_call(C, st, dp.slot);
+}
+
+int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                        const void *const *u, const void *const *d, const float *const *gs,
+                        const float *const *us, const float *const *ds, const float *xg,
+                        const int *xoff, const int *nr, const int *rows, const float *rw,
+                        float *out, int S, int act, float act_a, float act_b) {
+    (void)qgs;
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready) {
+        set_err("mvllm_hip_init not called");
+        return 0;
+    }
+    if (!args_ok(nb, D, fmt, xg, xoff, nr, out))
+        return 0;
+    Plan P;
+    build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
+    C.stats[0] += 1;
+    if (P.ew.empty())
+        return 1;
+    hipStream_t st = C.own;
+    if (!order_after_previous(C, st))
+        return 0;
+
+    // 1) resolve expert pieces: resident blobs first, misses copied into the arena
+    const size_t pb[4] = {piece_bytes(fmt, 0, D, Iinter), piece_bytes(fmt, 1, D, Iinter),
+                          piece_bytes(fmt, 2, D, Iinter), piece_bytes(fmt, 3, D, Iinter)};
+    std::vector<ExpertWork> hit, miss;
+    std::vector<std::vector<int>> hit_rows;  // unused; order kept by row0
+    std::vector<Resident *> touched;
+    std::vector<std::pair<const void *, size_t>> miss_src;  // per miss expert: 6 pieces
+    for (const ExpertWork &w0 : P.ew) {
+        ExpertWork w = w0;
+        bool all = true;
+        Resident *rs[6] = {};
+        for (int m = 0; m < 3 && all; ++m) {
+            rs[2 * m] = res_lookup(C, w.w[m]);
+            rs[2 * m + 1] = fmt ? res_lookup(C, w.s[m]) : rs[2 * m];
+            const size_t bw = pb[m == 2 ? 2 : 0], bs = pb[m == 2 ? 3 : 1];
+            all = rs[2 * m] &&
+                  static_cast<const uint8_t *>(w.w[m]) + bw <= rs[2 * m]->host + rs[2 * m]->bytes &&
+                  (!fmt || (rs[2 * m + 1] && static_cast<const uint8_t *>(w.s[m]) + bs <=
+                                                 rs[2 * m + 1]->host + rs[2 * m + 1]->bytes));
+        }
+        if (all) {
+            for (int m = 0; m < 3; ++m) {
+                w.w[m] = static_cast<uint8_t *>(rs[2 * m]->dev) +
+                         (static_cast<const uint8_t *>(w.w[m]) - rs[2 * m]->host);
+                if (fmt)
+                    w.s[m] = static_cast<uint8_t *>(rs[2 * m + 1]->dev) +
+                             (static_cast<const uint8_t *>(w.s[m]) - rs[2 * m + 1]->host);
+            }
+            for (auto *r : rs)
+                if (r) {
+                    HIP_TRY(hipStreamWaitEvent(st, r->ready, 0));
+                    touched.push_back(r);
+                    C.lru.splice(C.lru.begin(), C.lru, r->lru);
+                }
+            hit.push_back(w);
+            C.stats[6] += 1;
+        } else {
+            miss.push_back(w);
+            C.stats[7] += 1;
+        }
+    }
+    // 2) misses: copy their pieces on the copy stream into the arena
+    size_t per_expert = 0;
+    for (int m = 0; m < 3; ++m)
+        per_expert += ((pb[m == 2 ? 2 : 0] + 255) & ~size_t(255)) +
+                      (fmt ? ((pb[m == 2 ? 3 : 1] + 255) & ~size_t(255)) : 0);
+    hipEvent_t miss_ev = nullptr;
+    if (!miss.empty()) {
+        HIP_TRY(C.miss.ensure(per_expert * miss.size()));
+        uint8_t *arena = static_cast<uint8_t *>(C.miss.p);
+        size_t off = 0;
+        // the arena is reused per call: the copy stream waits for the previous call
+        if (C.have_last)
+            HIP_TRY(hipStreamWaitEvent(C.copy, C.last_done, 0));
+        for (ExpertWork &w : miss) {
+            for (int m = 0; m < 3; ++m) {
+                const size_t bw = pb[m == 2 ? 2 : 0], bs = pb[m == 2 ? 3 : 1];
+                HIP_TRY(hipMemcpyAsync(arena + off, w.w[m], bw, hipMemcpyHostToDevice, C.copy));
+                w.w[m] = arena + off;
+                off += (bw + 255) & ~size_t(255);
+                C.stats[2] += static_cast<double>(bw);
+                if (fmt) {
+                    HIP_TRY(hipMemcpyAsync(arena + off, w.s[m], bs, hipMemcpyHostToDevice, C.copy));
+                    w.s[m] = arena + off;
+                    off += (bs + 255) & ~size_t(255);
+                    C.stats[2] += static_cast<double>(bs);
+                }
+            }
+        }
+        HIP_TRY(hipEventCreateWithFlags(&miss_ev, hipEventDisableTiming));
+        HIP_TRY(hipEventRecord(miss_ev, C.copy));
+    }
+    // resident experts first, so their gate/up overlaps the miss copies
+    P.ew.clear();
+    P.ew.insert(P.ew.end(), hit.begin(), hit.end());
+    P.ew.insert(P.ew.end(), miss.begin(), miss.end());
+
+    // 3) activations: gather the compact rows into pinned memory, one H2D copy
+    const size_t R = P.xrow.size();
+    HIP_TRY(C.hx.ensure(R * D * 4));
+    HIP_TRY(C.Xc.ensure(R * D * 4));
+    for (size_t j = 0; j < R; ++j)
+        std::memcpy(static_cast<float *>(C.hx.p) + j * D, xg + (size_t)P.xrow[j] * D,
+                    (size_t)D * 4);
+    HIP_TRY(hipMemcpyAsync(C.Xc.p, C.hx.p, R * D * 4, hipMemcpyHostToDevice, st));
+    // 4) the destination rows of out, compacted (combine writes out_row = t)
+    const size_t T = P.out_row.size();
+    HIP_TRY(C.ho.ensure(T * D * 4));
+    HIP_TRY(C.Oc.ensure(T * D * 4));
+    for (size_t t = 0; t < T; ++t)
+        std::memcpy(static_cast<float *>(C.ho.p) + t * D, out + (size_t)P.out_row[t] * D,
+                    (size_t)D * 4);
+    HIP_TRY(hipMemcpyAsync(C.Oc.p, C.ho.p, T * D * 4, hipMemcpyHostToDevice, st));
+    C.stats[3] += static_cast<double>((R + T) * D * 4);
+    std::vector<int> dest_rows = P.out_row;
+    for (size_t t = 0; t < T; ++t)
+        P.out_row[t] = static_cast<int>(t);
+    DevPlan dp{};
+    if (!upload_plan(C, P, st, dp))
+        return 0;
+    const int ok = run_phases(C, P, dp, fmt, D, Iinter, act, act_a, act_b,
+                              static_cast<const float *>(C.Xc.p), nullptr,
+                              static_cast<float *>(C.Oc.p), st, hit.size(), miss_ev);
+    if (!ok)
+        return 0;
+    for (Resident *r : touched) {
+        HIP_TRY(hipEventRecord(r->last_use, st));
+        r->used = true;
+    }
+    HIP_TRY(hipMemcpyAsync(C.ho.p, C.Oc.p, T * D * 4, hipMemcpyDeviceToHost, st));
+    C.stats[4] += static_cast<double>(T * D * 4);
+    if (!finish_call(C, st, dp.slot))
+        return 0;
+    HIP_TRY(hipStreamSynchronize(st));
+    if (miss_ev)
+        (void)hipEventDestroy(miss_ev);
+    for (size_t t = 0; t < T; ++t)
+        std::memcpy(out + (size_t)dest_rows[t] * D, static_cast<float *>(C.ho.p) + t * D,
+                    (size_t)D * 4);
+    return 1;
+}
+
+void *mvllm_hip_host_alloc(size_t bytes) {
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        set_err("hipHostMalloc failed");
+        return nullptr;
+    }
+    return p;
+}
+
+void mvllm_hip_host_free(void *p) {
+    if (p)
+        (void)hipHostFree(p);
+}
+
+int mvllm_hip_set_expert_budget(size_t bytes) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    C.budget = bytes;
+    while (C.used_bytes > C.budget && !C.lru.empty())
+        res_drop(C, C.lru.back());
+    return 1;
+}
+
+int mvllm_hip_promote(const void *host_blob, size_t bytes, int layer, int eid) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !host_blob || bytes == 0) {
+        set_err("promote: not initialised or empty blob");
+        return 0;
+    }
+    const long long key = res_key(layer, eid);
+    auto it = C.res.find(key);
+    if (it != C.res.end()) {
+        if (it->second.host == host_blob && it->second.bytes == bytes) {
+            C.lru.splice(C.lru.begin(), C.lru, it->second.lru);
+            return 1;
+        }
+        res_drop(C, key);  // the store moved this expert to another slot
+    }
+    // a different expert previously promoted from an overlapping host range is stale
+    for (auto h = C.by_host.begin(); h != C.by_host.end();) {
+        const Resident &r = C.res[h->second];
+        const uint8_t *a = static_cast<const uint8_t *>(host_blob);
+        if (r.host < a + bytes && a < r.host + r.bytes) {
+            const long long k2 = h->second;
+            ++h;
+            res_drop(C, k2);
+        } else {
+            ++h;
+        }
+    }
+    while (C.used_bytes + bytes > C.budget && !C.lru.empty())
+        res_drop(C, C.lru.back());
+    if (C.used_bytes + bytes > C.budget) {
+        set_err("promote: blob larger than the expert budget");
+        return 0;
+    }
+    void *dev = res_alloc(C, bytes);
+    if (!dev) {
+        set_err("promote: hipMalloc failed");
+        return 0;
+    }
+    Resident r;
+    r.layer = layer;
+    r.eid = eid;
+    r.host = static_cast<const uint8_t *>(host_blob);
+    r.bytes = bytes;
+    r.dev = dev;
+    HIP_TRY(hipEventCreateWithFlags(&r.ready, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&r.last_use, hipEventDisableTiming));
+    HIP_TRY(hipMemcpyAsync(dev, host_blob, bytes, hipMemcpyHostToDevice, C.copy));
+    HIP_TRY(hipEventRecord(r.ready, C.copy));
+    C.lru.push_front(key);
+    r.lru = C.lru.begin();
+    C.res[key] = r;
+    C.by_host[r.host] = key;
+    C.used_bytes += bytes;
+    C.stats[5] += 1;
+    C.stats[2] += static_cast<double>(bytes);
+    return 1;
+}
+
+int mvllm_hip_evict(int layer, int eid) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    const long long key = res_key(layer, eid);
+    if (C.res.find(key) == C.res.end())
+        return 0;
+    res_drop(C, key);
+    return 1;
+}
+
+void *mvllm_hip_resident_ptr(int layer, int eid) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    auto it = C.res.find(res_key(layer, eid));
+    if (it == C.res.end())
+        return nullptr;
+    (void)hipEventSynchronize(it->second.ready);
+    return it->second.dev;
+}
+
+int mvllm_hip_stats(double *vals, int n) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    for (auto &t : C.timed) {
+        float ms[3] = {0, 0, 0};
+        (void)hipEventSynchronize(t.ev[3]);
+        for (int i = 0; i < 3; ++i)
+            (void)hipEventElapsedTime(&ms[i], t.ev[i], t.ev[i + 1]);
+        C.stats[9] += ms[0];
+        C.stats[10] += ms[1];
+        C.stats[11] += ms[2];
+        for (auto &e : t.ev)
+            (void)hipEventDestroy(e);
+    }
+    C.timed.clear();
+    const int m = std::min(n, 15);
+    for (int i = 0; i < m; ++i)
+        vals[i] = C.stats[i];
+    return m;
+}
+
+void mvllm_hip_stats_reset(void) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    for (auto &t : C.timed) {
+        (void)hipEventSynchronize(t.ev[3]);
+        for (auto &e : t.ev)
+            (void)hipEventDestroy(e);
+    }
+    C.timed.clear();
+    for (double &v : C.stats)
+        v = 0;
+}
+
+int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, int O, int K,
+                      float *w_dev) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || (fmt != 4 && fmt != 7) || O < 1 || K < 1 || !packed_dev || !scales_dev ||
+        !w_dev) {
+        set_err("dequant: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_dequant(fmt, packed_dev, scales_dev, O, K, w_dev, C.own));
+    HIP_TRY(hipStreamSynchronize(C.own));
+    return 1;
+}
+
+int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
+                             uint8_t *scales_dev) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !x_dev || !codes_dev || !scales_dev || n < 1 || K < 32 || K % 32) {
+        set_err("quantize_mxfp4: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev, C.own));
+    HIP_TRY(hipStreamSynchronize(C.own));
+    return 1;
+}
+
+}  // extern "C"

@@ -1,0 +1,205 @@
+"""Python binding of libmvllm_hip.so (the C ABI in include/mvllm_hip.h).
+
+The library is the product; this module only marshals arguments for tests and
+bench.py.  It never falls back to a CPU implementation: if the shared library is
+missing or the device is absent, calls raise.
+
+torch is imported before the library is loaded when it is installed: torch ships
+its own libamdhip64.so (SONAME libamdhip64.so.7), and loading ours first would put
+a second HIP runtime into the process.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+try:  # must precede CDLL (one HIP runtime per process)
+    import torch  # noqa: F401
+except ImportError:  # pragma: no cover - torch is part of this image
+    torch = None
+
+PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(PKG_DIR, "libmvllm_hip.so")
+HEADER = os.path.join(os.path.dirname(PKG_DIR), "include", "mvllm_hip.h")
+
+ACT_SILU, ACT_CLAMP_SWIGLU, ACT_SITU = 0, 1, 2
+STAT_NAMES = ["calls", "rows", "h2d_weight_bytes", "h2d_act_bytes", "d2h_bytes", "promotions",
+              "resident_hits", "misses", "evictions", "ms_gate_up", "ms_down", "ms_combine",
+              "ms_quantize", "launches_gate_up", "launches_down"]
+
+_i, _f, _p, _sz, _ll = C.c_int, C.c_float, C.c_void_p, C.c_size_t, C.c_longlong
+_pp = C.POINTER(C.c_void_p)
+
+_SIGS = {
+    "mvllm_hip_init": (_i, [_i]),
+    "mvllm_hip_shutdown": (None, []),
+    "mvllm_hip_available": (_i, []),
+    "mvllm_hip_name": (C.c_char_p, []),
+    "mvllm_hip_last_error": (C.c_char_p, []),
+    "mvllm_hip_moe_block": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p, _p, _p, _p,
+                                 _p, _p, _i, _i, _f, _f]),
+    "mvllm_hip_moe_block_dev": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p, _p,
+                                     _p, _p, _p, _p, _i, _i, _f, _f, _p]),
+    "mvllm_hip_set_option": (_i, [C.c_char_p, _ll]),
+    "mvllm_moe_union_ids": (_i, [_p, _i, _i, _p, _i]),
+    "mvllm_moe_segments": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
+    "mvllm_expert_geom": (_ll, [_i, _i, _i, _p]),
+    "mvllm_hip_host_alloc": (_p, [_sz]),
+    "mvllm_hip_host_free": (None, [_p]),
+    "mvllm_hip_set_expert_budget": (_i, [_sz]),
+    "mvllm_hip_promote": (_i, [_p, _sz, _i, _i]),
+    "mvllm_hip_evict": (_i, [_i, _i]),
+    "mvllm_hip_resident_ptr": (_p, [_i, _i]),
+    "mvllm_hip_stats": (_i, [_p, _i]),
+    "mvllm_hip_stats_reset": (None, []),
+    "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
+    "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load libmvllm_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run __graft_entry__.build() first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype, fn.argtypes = res, args
+        _lib = L
+    return _lib
+
+
+def header_symbols():
+    """Every function name the public header declares."""
+    import re
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(mvllm_[a-z0-9_]+)\s*\(", text)))
+
+
+class HipError(RuntimeError):
+    pass
+
+
+def _check(rc, what):
+    if rc != 1:
+        raise HipError(f"{what} failed: {lib().mvllm_hip_last_error().decode()}")
+
+
+def init(device: int = 0):
+    _check(lib().mvllm_hip_init(device), "mvllm_hip_init")
+
+
+def shutdown():
+    lib().mvllm_hip_shutdown()
+
+
+def set_option(key: str, value: int) -> bool:
+    return lib().mvllm_hip_set_option(key.encode(), int(value)) == 1
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()  # torch tensor
+
+
+def _ptr_array(items):
+    arr = (C.c_void_p * len(items))()
+    for i, a in enumerate(items):
+        arr[i] = None if a is None else (a if isinstance(a, int) else _ptr(a))
+    return arr
+
+
+def moe_block(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
+              act=ACT_SILU, act_a=0.0, act_b=0.0, qgs=0, check=True):
+    """Host-pointer drop-in (numpy arrays).  Lists may hold None; any list may be None."""
+    pa = [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
+    rc = lib().mvllm_hip_moe_block(nb, D, Iinter, fmt, qgs, *pa, _ptr(xg), _ptr(xoff), _ptr(nr),
+                                   _ptr(rows), _ptr(rw), _ptr(out), S, act, act_a, act_b)
+    if check:
+        _check(rc, "mvllm_hip_moe_block")
+    return rc
+
+
+def moe_block_dev(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
+                  act=ACT_SILU, act_a=0.0, act_b=0.0, stream=None, check=True):
+    """Device variant: g..ds are lists of device pointers (ints) or torch tensors;
+    xg/out are torch CUDA tensors; xoff/nr/rows/rw are numpy host arrays."""
+    pa = [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
+    st = None if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+    rc = lib().mvllm_hip_moe_block_dev(nb, D, Iinter, fmt, 0, *pa, _ptr(xg), _ptr(xoff),
+                                       _ptr(nr), _ptr(rows), _ptr(rw), _ptr(out), S, act, act_a,
+                                       act_b, st)
+    if check:
+        _check(rc, "mvllm_hip_moe_block_dev")
+    return rc
+
+
+def union_ids(idx, n_tok, topk, cap):
+    idx = np.ascontiguousarray(idx, np.int32)
+    out = np.full(max(cap, 1), -7, np.int32)
+    n = lib().mvllm_moe_union_ids(_ptr(idx), n_tok, topk, _ptr(out), cap)
+    return out[:n]
+
+
+def segments(idx, wt, n_tok, topk, cap_experts):
+    """-> (nb, eids, xoff, nr, rows, rw) for one batched moe_block call."""
+    idx = np.ascontiguousarray(idx, np.int32)
+    wt = np.ascontiguousarray(wt, np.float32)
+    cap_rows = max(n_tok * topk, 1)
+    eids = np.zeros(cap_experts, np.int32)
+    xoff = np.zeros(cap_experts, np.int32)
+    nr = np.zeros(cap_experts, np.int32)
+    rows = np.zeros(cap_rows, np.int32)
+    rw = np.zeros(cap_rows, np.float32)
+    nrows = np.zeros(1, np.int32)
+    nb = lib().mvllm_moe_segments(_ptr(idx), _ptr(wt), n_tok, topk, _ptr(eids), _ptr(xoff),
+                                  _ptr(nr), _ptr(rows), _ptr(rw), cap_experts, cap_rows,
+                                  _ptr(nrows))
+    if nb < 0:
+        raise HipError("mvllm_moe_segments: capacity too small")
+    j = int(nrows[0])
+    return nb, eids[:nb], xoff[:nb], nr[:nb], rows[:j], rw[:j]
+
+
+def expert_geom(fmt, D, Iinter):
+    """-> (blob_bytes, offsets[6] = gate_p, gate_s, up_p, up_s, down_p, down_s)."""
+    off = np.zeros(6, np.int64)
+    n = lib().mvllm_expert_geom(fmt, D, Iinter, _ptr(off))
+    return int(n), off
+
+
+def promote(host_blob_ptr: int, nbytes: int, layer: int, eid: int):
+    _check(lib().mvllm_hip_promote(host_blob_ptr, nbytes, layer, eid), "mvllm_hip_promote")
+
+
+def evict(layer, eid) -> bool:
+    return lib().mvllm_hip_evict(layer, eid) == 1
+
+
+def stats():
+    v = np.zeros(len(STAT_NAMES), np.float64)
+    n = lib().mvllm_hip_stats(_ptr(v), len(v))
+    return dict(zip(STAT_NAMES[:n], v[:n].tolist()))
+
+
+def stats_reset():
+    lib().mvllm_hip_stats_reset()
+
+
+def dequant(fmt, packed_dev, scales_dev, O, K, w_dev):
+    _check(lib().mvllm_hip_dequant(fmt, _ptr(packed_dev), _ptr(scales_dev), O, K, _ptr(w_dev)),
+           "mvllm_hip_dequant")
+
+
+def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):
+    _check(lib().mvllm_hip_quantize_mxfp4(_ptr(x_dev), n, K, _ptr(codes_dev), _ptr(scales_dev)),
+           "mvllm_hip_quantize_mxfp4")

@@ -1,0 +1,309 @@
+"""GPU parity: the HIP library (through its C ABI) against the CPU oracle.
+
+Bars: dequantized weights, MXFP4 activation codes/scales and segment arrays are
+bit-exact; the f32 GEMV path (decode) is within 2e-5 relative (max|y-ref| / max|ref|)
+of the oracle, which itself equals the reference build bit for bit.
+"""
+import ctypes
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import npref
+from cases import random_case
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 2e-5
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return None if a is None else torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dev_lists(c):
+    keep = []
+
+    def L(xs):
+        if xs is None:
+            return None
+        out = []
+        for x in xs:
+            t = dev(x)
+            keep.append(t)
+            out.append(None if t is None else t.data_ptr())
+        return out
+    return [L(c.g), L(c.u), L(c.d), L(c.gs), L(c.us), L(c.ds)], keep
+
+
+def run_dev(hip, c, act, a, b, stream=None):
+    lists, keep = dev_lists(c)
+    xg = dev(c.xg)
+    out = dev(c.out)
+    hip.moe_block_dev(c.nb, c.D, c.I, c.fmt, *lists, xg, c.xoff, c.nr, c.rows, c.rw, out, c.S,
+                      act, a, b, stream=stream)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_out(orc, c, act, a, b):
+    o = c.out.copy()
+    assert orc.moe_block(*c.args(o), act, a, b) == 1
+    return o
+
+
+# ------------------------------------------------------------- bit-exact formats
+
+@pytest.mark.parametrize("fmt,O,K,offset", [(4, 64, 2048, 0), (4, 33, 1024, 0), (4, 9, 96, 0),
+                                            (4, 5, 77, 0), (4, 8, 256, 3), (7, 64, 7168, 0),
+                                            (7, 17, 2048, 0), (7, 6, 45, 0), (7, 8, 256, 1)])
+def test_dequant_bit_exact(hip, orc, fmt, O, K, offset):
+    say("dequant", fmt, O, K, offset)
+    rng = np.random.default_rng(O * K + fmt)
+    packed = rng.integers(0, 256, size=(O, (K + 1) // 2), dtype=np.uint8)
+    if fmt == 4:
+        scales = rng.uniform(-0.03, 0.03, size=(O, (K + 63) // 64)).astype(np.float32)
+        scales.flat[::7] = 0.0
+    else:
+        scales = rng.integers(0, 256, size=(O, (K + 31) // 32), dtype=np.uint8)
+    # offset > 0 misaligns the packed base and forces the element-wise path
+    pbuf = torch.zeros(packed.size + 16, dtype=torch.uint8, device="cuda")
+    pbuf[offset:offset + packed.size] = torch.from_numpy(packed.ravel()).cuda()
+    s_d = dev(scales)
+    w = torch.empty((O, K), dtype=torch.float32, device="cuda")
+    hip.dequant(fmt, pbuf[offset:], s_d, O, K, w)
+    got = w.cpu().numpy()
+    exp = orc.dequant(fmt, packed, scales, O, K)
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+    m = ~np.isnan(exp)
+    assert np.array_equal(got[m].view(np.uint32), exp[m].view(np.uint32))
+
+
+def test_quantize_mxfp4_bit_exact(hip, orc):
+    say("quantize_mxfp4")
+    rng = np.random.default_rng(77)
+    n, K = 12, 512
+    x = rng.standard_normal((n, K)) * np.repeat(np.exp2(rng.integers(-40, 40, (n, K // 32))),
+                                                 32, axis=1)
+    x = x.astype(np.float32)
+    x[0, :32] = 0.0
+    x[1, 5], x[2, 7], x[3, 9] = np.nan, np.inf, -np.inf
+    x[4, :32] = np.float32(0.25) * (np.arange(32) % 13)  # exact ties between codes
+    codes = torch.zeros((n, K // 2), dtype=torch.uint8, device="cuda")
+    scales = torch.zeros((n, K // 32), dtype=torch.uint8, device="cuda")
+    hip.quantize_mxfp4(dev(x), n, K, codes, scales)
+    cg, sg = codes.cpu().numpy(), scales.cpu().numpy()
+    for r in range(n):
+        rc, _, sc, cd = orc.fp4_activation_qdq(x[r], 32)
+        assert np.array_equal(sg[r], sc), r
+        assert np.array_equal(npref.unpack_nibbles(cg[r:r + 1], K)[0], cd), r
+
+
+# ------------------------------------------------------------- f32 GEMV parity
+
+DEV_CASES = [
+    # fmt, D, I, nr, S, act, a, b, null_experts, invalid_rows
+    (4, 1024, 512, [1, 1], 1, 1, 7.0, 0.0, (), 0),                 # c0 shape
+    (4, 2048, 1024, [1] * 8, 1, 0, 0.0, 0.0, (), 0),               # c1 T=1 shape
+    (4, 2048, 1024, [2, 3, 1, 4, 2], 4, 0, 0.0, 0.0, (), 0),       # NR 4
+    (4, 512, 256, [8, 5, 16, 1], 16, 1, 7.0, 0.0, (), 0),          # NR 8 and > 8 rows
+    (4, 256, 128, [1, 2, 0, 3], 4, 1, 7.0, 0.0, (1,), 2),          # skips + invalid rows
+    (4, 96, 70, [2, 1], 3, 1, 0.0, 0.0, (), 0),                    # odd I: generic down
+    (4, 77, 33, [1, 2], 2, 0, 0.0, 0.0, (), 0),                    # odd everything
+    (7, 7168, 2048, [1, 1, 1], 1, 2, 4.0, 25.0, (), 0),            # c2 shape
+    (7, 1024, 512, [3, 1, 2, 6], 6, 2, 4.0, 25.0, (), 1),
+    (7, 65, 31, [1, 1], 2, 2, 4.0, 25.0, (), 0),
+    (0, 64, 48, [2, 1], 3, 1, 3.0, 0.0, (0,), 0),                  # f32 weights
+]
+
+
+@pytest.mark.parametrize("case", DEV_CASES)
+def test_moe_block_dev_parity(hip, orc, case):
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("moe_block_dev", case)
+    rng = np.random.default_rng(D * 31 + I + len(nr))
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    got = run_dev(hip, c, act, a, b)
+    exp = oracle_out(orc, c, act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < TOL_F32
+
+
+@pytest.mark.parametrize("case", DEV_CASES[::2])
+def test_moe_block_host_parity(hip, orc, case):
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("moe_block host", case)
+    rng = np.random.default_rng(D * 37 + I)
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    got = c.out.copy()
+    assert hip.moe_block(*c.args(got), act, a, b) == 1
+    exp = oracle_out(orc, c, act, a, b)
+    assert npref.rel_err(got, exp) < TOL_F32
+    # rows that receive nothing are untouched bit for bit
+    touched = set(int(r) for r in c.rows if 0 <= r < c.S)
+    for t in range(c.out.shape[0]):
+        if t not in touched:
+            assert np.array_equal(got[t], c.out[t])
+
+
+def test_validation_matches_reference(hip):
+    say("validation")
+    rng = np.random.default_rng(5)
+    c = random_case(rng, 4, 64, 64, [1], 1)
+    for k, v in ((0, 0), (1, 0), (3, 5), (10, None), (11, None), (12, None), (15, None)):
+        args = list(c.args())
+        args[k] = v
+        assert hip.moe_block(*args, 0, 0.0, 0.0, check=False) == 0
+    args = list(c.args())
+    args[13] = None  # rows == NULL: nothing reaches out
+    o = args[15]
+    assert hip.moe_block(*args, 0, 0.0, 0.0) == 1 and np.array_equal(o, c.out)
+
+
+def test_nonfinite_propagation(hip, orc):
+    """Inf scales / activations take the exact per-element path: NaN and Inf land
+    where the reference puts them."""
+    say("nonfinite")
+    rng = np.random.default_rng(8)
+    for fmt in (4, 7):
+        c = random_case(rng, fmt, 256, 128, [1, 1, 1], 3, 2 if fmt == 7 else 1, 4.0, 25.0)
+        c.rows[:] = [0, 1, 2]
+        if fmt == 7:
+            c.gs[0][5, 2] = 255      # +inf scale in one gate group of expert 0
+            c.ds[1][7, 1] = 0        # zero scale in one down group of expert 1
+        else:
+            c.gs[0][5, 1] = np.inf
+            c.ds[1][7, 0] = -np.inf
+        c.xg[2, 17] = np.inf
+        got = run_dev(hip, c, c.act, c.a, c.b)
+        exp = oracle_out(orc, c, c.act, c.a, c.b)
+        assert np.array_equal(np.isnan(got), np.isnan(exp))
+        assert np.array_equal(np.isinf(got), np.isinf(exp))
+        fin = np.isfinite(exp)
+        assert np.array_equal(np.sign(got[np.isinf(exp)]), np.sign(exp[np.isinf(exp)]))
+        assert npref.rel_err(got[fin], exp[fin]) < TOL_F32
+
+
+# ------------------------------------------------------------- benchmark configs
+
+@pytest.mark.parametrize("name,T", [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 16), ("c2", 1)])
+def test_config_parity(hip, orc, name, T):
+    from mvllm_hip import synth
+    say("config", name, T)
+    w = synth.make_workload(name, T=T)
+    g, u, d, gs, us, ds = w.lists()
+    out = np.zeros((T, w.D), np.float32)
+    exp = out.copy()
+    assert orc.moe_block(w.nb, w.D, w.I, w.fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows,
+                         w.rw, exp, T, w.act, w.a, w.b) == 1
+    from cases import Case
+    c = Case(w.nb, w.D, w.I, w.fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, out,
+             T, w.act, w.a, w.b)
+    got = run_dev(hip, c, w.act, w.a, w.b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < TOL_F32
+    # the drop-in host entry gives the same result
+    got2 = out.copy()
+    hip.moe_block(w.nb, w.D, w.I, w.fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw,
+                  got2, T, w.act, w.a, w.b)
+    assert npref.rel_err(got2, exp) < TOL_F32
+
+
+# ------------------------------------------------------------- residency / staging
+
+def test_promote_hits_and_evict(hip, orc):
+    from mvllm_hip import synth
+    say("promote")
+    w = synth.make_workload("c0", T=1)
+    n, off = hip.expert_geom(4, w.D, w.I)
+    blobs = []
+    L = hip.lib()
+    for e in w.eids:
+        p = L.mvllm_hip_host_alloc(n)
+        assert p
+        buf = (ctypes.c_uint8 * n).from_address(p)
+        arr = np.frombuffer(buf, np.uint8)
+        ex = w.experts[int(e)]
+        for piece, o in zip(("gp", "gs", "up", "us", "dp", "ds"), off):
+            b = ex[piece].view(np.uint8).ravel()
+            arr[o:o + b.size] = b
+        blobs.append((p, arr))
+    views = []
+    for p, arr in blobs:
+        v = {}
+        for piece, o in zip(("gp", "gs", "up", "us", "dp", "ds"), off):
+            src = w.experts[int(w.eids[0])][piece]
+            v[piece] = np.frombuffer((ctypes.c_uint8 * (src.nbytes)).from_address(p + int(o)),
+                                     src.dtype).reshape(src.shape)
+        views.append(v)
+    g = [v["gp"] for v in views]
+    u = [v["up"] for v in views]
+    d = [v["dp"] for v in views]
+    gs = [v["gs"] for v in views]
+    us = [v["us"] for v in views]
+    ds = [v["ds"] for v in views]
+    exp = np.zeros((1, w.D), np.float32)
+    orc.moe_block(w.nb, w.D, w.I, 4, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, exp,
+                  1, w.act, w.a, w.b)
+    hip.stats_reset()
+    # 1) nothing resident: misses, copied in
+    o1 = np.zeros((1, w.D), np.float32)
+    hip.moe_block(w.nb, w.D, w.I, 4, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, o1,
+                  1, w.act, w.a, w.b)
+    st = hip.stats()
+    assert st["misses"] == w.nb and st["resident_hits"] == 0
+    # 2) promote both: hits
+    for i, (p, arr) in enumerate(blobs):
+        hip.promote(p, n, 0, int(w.eids[i]))
+    o2 = np.zeros((1, w.D), np.float32)
+    hip.moe_block(w.nb, w.D, w.I, 4, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, o2,
+                  1, w.act, w.a, w.b)
+    st = hip.stats()
+    assert st["resident_hits"] == w.nb and st["promotions"] == w.nb
+    assert npref.rel_err(o1, exp) < TOL_F32 and npref.rel_err(o2, exp) < TOL_F32
+    # 3) evict one: one hit, one miss; the slot's new content is picked up
+    assert hip.evict(0, int(w.eids[0]))
+    blobs[0][1][:] = blobs[1][1][:]  # the store reused slot 0 for expert eids[1]
+    o3 = np.zeros((1, w.D), np.float32)
+    hip.moe_block(w.nb, w.D, w.I, 4, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, o3,
+                  1, w.act, w.a, w.b)
+    g2, u2, d2 = [g[1], g[1]], [u[1], u[1]], [d[1], d[1]]
+    gs2, us2, ds2 = [gs[1], gs[1]], [us[1], us[1]], [ds[1], ds[1]]
+    exp3 = np.zeros((1, w.D), np.float32)
+    orc.moe_block(w.nb, w.D, w.I, 4, g2, u2, d2, gs2, us2, ds2, w.xg, w.xoff, w.nr, w.rows, w.rw,
+                  exp3, 1, w.act, w.a, w.b)
+    assert npref.rel_err(o3, exp3) < TOL_F32
+    for p, _ in blobs:
+        L.mvllm_hip_host_free(p)
+    for e in w.eids:
+        hip.evict(0, int(e))
+
+
+def test_two_streams_in_sequence(hip, orc):
+    say("two streams")
+    rng = np.random.default_rng(44)
+    c1 = random_case(rng, 4, 1024, 512, [2, 1, 3], 4, 1, 7.0, 0.0)
+    c2 = random_case(rng, 7, 1024, 512, [1, 2], 4, 2, 4.0, 25.0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    l1, k1 = dev_lists(c1)
+    l2, k2 = dev_lists(c2)
+    x1, o1 = dev(c1.xg), dev(c1.out)
+    x2, o2 = dev(c2.xg), dev(c2.out)
+    torch.cuda.synchronize()
+    hip.moe_block_dev(c1.nb, c1.D, c1.I, 4, *l1, x1, c1.xoff, c1.nr, c1.rows, c1.rw, o1, c1.S,
+                      1, 7.0, 0.0, stream=s1)
+    hip.moe_block_dev(c2.nb, c2.D, c2.I, 7, *l2, x2, c2.xoff, c2.nr, c2.rows, c2.rw, o2, c2.S,
+                      2, 4.0, 25.0, stream=s2)
+    torch.cuda.synchronize()
+    assert npref.rel_err(o1.cpu().numpy(), oracle_out(orc, c1, 1, 7.0, 0.0)) < TOL_F32
+    assert npref.rel_err(o2.cpu().numpy(), oracle_out(orc, c2, 2, 4.0, 25.0)) < TOL_F32
