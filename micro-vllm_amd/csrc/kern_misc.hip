@@ -70,10 +70,14 @@ __device__ __forceinline__ int nearest_e2m1(float v) {
     return best;
 }
 
-// ceil(log2(v)) for a normal v > 0 (frexp exponent, minus one at exact powers of two)
+// ceil(log2(v)) for v >= 2^-126 (frexp exponent, minus one at exact powers of two).
+// An infinite v (a block holding +-Inf) gives 0: frexp leaves the exponent at 0 for
+// non-finite input, which is what the reference's ceil_log2_positive then returns.
 __device__ __forceinline__ int ceil_log2_normal(float v) {
     const uint32_t b = __float_as_uint(v);
     const int ef = (int)((b >> 23) & 0xffu);
+    if (ef == 255)
+        return 0;
     return (b & 0x7fffffu) == 0 ? ef - 127 : ef - 126;
 }
 
