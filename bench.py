@@ -100,24 +100,22 @@ def main():
                 ptrs[slot].append(b + int(off[oi]))
         return ptrs
 
-    layer_lists = [lists(l) for l in range(layers)]
+    layer_lists = [mvllm_hip.prepare_lists(*lists(l)) for l in range(layers)]
     xg = torch.from_numpy(w.xg).cuda()
     out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    xoff, nr, rows, rw = w.xoff, w.nr, w.rows, w.rw
 
     def step(s):
-        g, u, d, gs, us, ds = layer_lists[s % layers]
-        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, g, u, d, gs, us, ds, xg, w.xoff, w.nr, w.rows,
-                                w.rw, out, T, w.act, w.a, w.b)
+        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, xg, xoff,
+                                nr, rows, rw, out, T, w.act, w.a, w.b,
+                                prepared=layer_lists[s % layers])
 
     for s in range(args.warmup):
         step(s)
     torch.cuda.synchronize()
 
-    # timed region: K steps bracketed by synchronize; per-kernel HIP events are recorded
-    # by the library on the same stream
-    mvllm_hip.set_option("timing", 1)
-    mvllm_hip.stats_reset()
-    torch.cuda.synchronize()
+    # timed region: K steps bracketed by synchronize (torch's stream = the null stream,
+    # which the library's kernels run on)
     t0 = time.perf_counter()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record()
@@ -127,6 +125,14 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = ev0.elapsed_time(ev1) / args.steps
+
+    # per-kernel durations: a second pass with the library's HIP events around each
+    # phase, recorded on the stream the kernels are launched on
+    mvllm_hip.set_option("timing", 1)
+    mvllm_hip.stats_reset()
+    for s in range(args.steps):
+        step(s)
+    torch.cuda.synchronize()
     st = mvllm_hip.stats()
     mvllm_hip.set_option("timing", 0)
     ms_gu = st["ms_gate_up"] / args.steps

@@ -74,17 +74,18 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
                             const int *nr, const int *rows, const float *rw, float *out, int S,
                             int act, float act_a, float act_b, void *stream);
 
-/* Numerics mode for segments of many rows (prefill).  The decode GEMV (segments
- * of <= mvllm_hip_set_option("mfma_min_rows") rows) always accumulates in f32.
- *   0  auto: f32 GEMV for short segments, bf16 MFMA for long ones (default)
- *   1  f32 everywhere (exact-order-independent f32 GEMV; slow for prefill)
- *   2  bf16 MFMA for every segment of fmt 4 / 7
- *   3  like 0, but fmt 7 long segments quantize activations to MXFP4
- *      (fp4_activation_qdq semantics, src/quant/native_act.cpp:159-179) and run
- *      the gfx950 scaled FP4 MFMA.
- * Options (key, value): "mode" (above), "mfma_min_rows" (default 32),
- * "timing" (1 = record per-kernel HIP events; read them with mvllm_hip_stats).
- * Returns 1 if the key is known. */
+/* Options (key, value); returns 1 if the key and value are accepted.
+ *   "mode"   how activations enter the matrix cores (weights are always decoded
+ *            exactly; products and sums are f32):
+ *            0  default: each f32 activation as 2 bf16 terms (hi + lo; represents the
+ *               value to 2^-17 relative, below the reference's own f32 summation noise)
+ *            1  3 bf16 terms (the activation exactly)
+ *            2  1 bf16 term (bf16 activations; ~2^-9 relative)
+ *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
+ *   "dec_ks" 0 = automatic; 1, 2 or 4 forces the split of K across waves.
+ *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
+ * Shapes the matrix-core kernels do not take (fmt 0, D or Iinter not a multiple of
+ * 1024 or above 8192, misaligned pointers) run an exact f32 kernel instead. */
 int mvllm_hip_set_option(const char *key, long long value);
 
 /* ---- segment construction: moe_union_ids (src/model/ops.cpp:1082-1099) and the
@@ -163,6 +164,16 @@ int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, i
  * K must be a multiple of 32.  Synchronous.  1 ok. */
 int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
                              uint8_t *scales_dev);
+
+/* Memory-system probe used to calibrate the roofline (no reference counterpart):
+ * kind 0 streams `bytes` of src_dev with coalesced 16-byte reads, kind 1 copies them to
+ * dst_dev, kinds 2..6 walk rows of row_bytes (a multiple of 1024) the way a wave walks
+ * expert weight rows: 2 = 16 rows x 32 B per load (8-byte lanes), 3 = 32 rows x 32 B,
+ * 4 = 16 rows x 64 B, 5 = 4 rows x 256 B, 6 = 1 row x 1 KB (16-byte lanes); dst_dev
+ * receives a sink word.
+ * Runs `reps` times on the backend's stream; *ms_per_rep gets the mean time.  1 ok. */
+int mvllm_hip_membench(int kind, const void *src_dev, void *dst_dev, size_t bytes, int row_bytes,
+                       int reps, double *ms_per_rep);
 
 #ifdef __cplusplus
 }

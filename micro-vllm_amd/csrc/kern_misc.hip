@@ -8,28 +8,41 @@ namespace mvllm_hip {
 // out[t] += w_e * Y[e] for the token's entries in reference order (expert order, then
 // row order), each step rounded as `orow[i] += w * hr[i]` rounds on the host
 // (src/gpu/metal_ops.cpp:328-339): a product, then a sum, no fused multiply-add.
-__global__ __launch_bounds__(256) void k_combine(CombineArgs A) {
+// The entries' loads are issued in batches of 8 before the ordered accumulation.
+__global__ __launch_bounds__(64) void k_combine(CombineArgs A) {
     const int t = blockIdx.y;
     const int e0 = A.tok_ptr[t], e1 = A.tok_ptr[t + 1];
     float *orow = A.out + (size_t)A.out_row[t] * (size_t)A.D;
     if ((A.D & 3) == 0 && ((uintptr_t)A.out & 15) == 0) {
-        const int d4 = blockIdx.x * 256 + threadIdx.x;
+        const int d4 = blockIdx.x * 64 + threadIdx.x;
         if (d4 * 4 >= A.D)
             return;
         float4 o = reinterpret_cast<float4 *>(orow)[d4];
-        for (int e = e0; e < e1; ++e) {
-            const float w = A.ent_w[e];
-            const float4 y =
-                reinterpret_cast<const float4 *>(A.Y + (size_t)A.ent_row[e] * (size_t)A.D)[d4];
-            o.x = __fadd_rn(o.x, __fmul_rn(w, y.x));
-            o.y = __fadd_rn(o.y, __fmul_rn(w, y.y));
-            o.z = __fadd_rn(o.z, __fmul_rn(w, y.z));
-            o.w = __fadd_rn(o.w, __fmul_rn(w, y.w));
+        for (int eb = e0; eb < e1; eb += 8) {
+            float4 y[8];
+            float w[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (eb + i < e1) {
+                    w[i] = A.ent_w[eb + i];
+                    y[i] = reinterpret_cast<const float4 *>(
+                        A.Y + (size_t)A.ent_row[eb + i] * (size_t)A.D)[d4];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (eb + i < e1) {
+                    o.x = __fadd_rn(o.x, __fmul_rn(w[i], y[i].x));
+                    o.y = __fadd_rn(o.y, __fmul_rn(w[i], y[i].y));
+                    o.z = __fadd_rn(o.z, __fmul_rn(w[i], y[i].z));
+                    o.w = __fadd_rn(o.w, __fmul_rn(w[i], y[i].w));
+                }
+            }
         }
         reinterpret_cast<float4 *>(orow)[d4] = o;
     } else {
-        for (int d = blockIdx.x * 1024 + threadIdx.x; d < A.D && d < (blockIdx.x + 1) * 1024;
-             d += 256) {
+        for (int d = blockIdx.x * 256 + threadIdx.x; d < A.D && d < (blockIdx.x + 1) * 256;
+             d += 64) {
             float o = orow[d];
             for (int e = e0; e < e1; ++e)
                 o = __fadd_rn(o, __fmul_rn(A.ent_w[e], A.Y[(size_t)A.ent_row[e] * A.D + d]));
@@ -41,7 +54,7 @@ __global__ __launch_bounds__(256) void k_combine(CombineArgs A) {
 hipError_t launch_combine(const CombineArgs &a, hipStream_t st) {
     if (a.n_tok <= 0)
         return hipSuccess;
-    const dim3 grid((unsigned)((a.D + 1023) / 1024), (unsigned)a.n_tok), block(256);
+    const dim3 grid((unsigned)((a.D + 255) / 256), (unsigned)a.n_tok), block(64);
     hipLaunchKernelGGL(k_combine, grid, block, 0, st, a);
     return hipGetLastError();
 }
@@ -115,6 +128,84 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
     if (n <= 0 || K <= 0 || K % 32)
         return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_quantize_mxfp4, dim3(1024), dim3(256), 0, st, x, n, K, codes, scales);
+    return hipGetLastError();
+}
+
+// ---- memory probes (roofline calibration) -------------------------------------------
+
+// kind 0: coalesced 16-byte reads of n16 uint4 (grid-stride); the xor keeps them live.
+// kind 2..: a wave walks a tile of rows (row16 uint4 per row) as the expert weights are
+// walked; pattern = kind - 2 selects (bytes per lane, lanes per row):
+//   0: (8, 4)  -> 16 rows x 32 B per load      1: (16, 2) -> 32 rows x 32 B
+//   2: (16, 4) -> 16 rows x 64 B               3: (16, 16) -> 4 rows x 256 B
+//   4: (16, 64) -> 1 row x 1 KB
+template <int LB, int LPR>
+__device__ __forceinline__ uint32_t walk_rows(const uint4 *src, size_t n16, int row16) {
+    constexpr int RPI = 64 / LPR;  // rows per load instruction
+    const int lane = threadIdx.x & 63;
+    const size_t wave = (blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6;
+    const size_t nwaves = ((size_t)gridDim.x * blockDim.x) >> 6;
+    const size_t tile16 = (size_t)RPI * row16;
+    const size_t ntiles = n16 / tile16;
+    const int step = LPR * LB;  // bytes per row per load
+    uint32_t acc = 0;
+    const uint8_t *s8 = reinterpret_cast<const uint8_t *>(src);
+    for (size_t t = wave; t < ntiles; t += nwaves) {
+        const uint8_t *row = s8 + (t * tile16 + (size_t)(lane / LPR) * row16) * 16 + (lane % LPR) * LB;
+#pragma unroll 8
+        for (int c = 0; c < row16 * 16; c += step) {
+            if constexpr (LB == 8) {
+                const uint2 v = *reinterpret_cast<const uint2 *>(row + c);
+                acc ^= v.x ^ v.y;
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4 *>(row + c);
+                acc ^= v.x ^ v.y ^ v.z ^ v.w;
+            }
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void k_stream_read(const uint4 *src, size_t n16, int kind,
+                                                     int row16, uint32_t *sink) {
+    uint32_t acc = 0;
+    if (kind == 0) {
+        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
+             i += (size_t)gridDim.x * blockDim.x) {
+            const uint4 v = src[i];
+            acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        }
+    } else if (kind == 2) {
+        acc = walk_rows<8, 4>(src, n16, row16);
+    } else if (kind == 3) {
+        acc = walk_rows<16, 2>(src, n16, row16);
+    } else if (kind == 4) {
+        acc = walk_rows<16, 4>(src, n16, row16);
+    } else if (kind == 5) {
+        acc = walk_rows<16, 16>(src, n16, row16);
+    } else {
+        acc = walk_rows<16, 64>(src, n16, row16);
+    }
+    if (acc == 0x9e3779b9u)  // practically never; keeps the loads
+        sink[0] = acc;
+}
+
+__global__ __launch_bounds__(256) void k_stream_copy(const uint4 *src, uint4 *dst, size_t n16) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n16;
+         i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, int row16,
+                           hipStream_t st) {
+    const size_t n16 = bytes / 16;
+    const dim3 grid(256 * 16), block(256);
+    if (kind == 1)
+        hipLaunchKernelGGL(k_stream_copy, grid, block, 0, st, static_cast<const uint4 *>(src),
+                           static_cast<uint4 *>(dst), n16);
+    else
+        hipLaunchKernelGGL(k_stream_read, grid, block, 0, st, static_cast<const uint4 *>(src), n16,
+                           kind, row16, static_cast<uint32_t *>(dst));
     return hipGetLastError();
 }
 

@@ -45,28 +45,39 @@ struct CombineArgs {
 
 enum : int { ACT_SILU = 0, ACT_CLAMP_SWIGLU = 1, ACT_SITU = 2 };
 
-// Launchers (kern_gemv.hip / kern_misc.hip).  All return hipSuccess or the launch error.
-// Fast GEMV: fmt 4 or 7, K % 32 == 0, 16-byte aligned packed rows.
-hipError_t launch_gemv_fast(int fmt, bool dual, int nr_max, int lanes_per_row, int passes,
-                            const GemvArgs &a, hipStream_t st);
+// Launchers (kern_gemv.hip / kern_misc.hip / kern_mfma.hip).  All return hipSuccess or
+// the launch error.
 // Generic GEMV: any K, any alignment, fmt 0/4/7 (exact reference per-element formula).
 hipError_t launch_gemv_generic(int fmt, bool dual, const GemvArgs &a, hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t st);
 hipError_t launch_dequant(int fmt, const void *packed, const void *scales, int O, int K,
                           float *w, hipStream_t st);
+hipError_t launch_dequant_bf16path(int fmt, const void *packed, const void *scales, int O,
+                                   int K, float *w, hipStream_t st);
+hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, int row16,
+                           hipStream_t st);
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st);
 
-// Output rows one fast-GEMV workgroup covers for the given lanes_per_row / passes.
-inline int gemv_rows_per_tile(int lanes_per_row, int passes) {
-    return 4 * (64 / lanes_per_row) * passes;
-}
-// LDS bytes the fast GEMV stages per K-slice (one row: 36 floats per 32 inputs).
-constexpr int kGemvLdsBytes = 36864;
-inline int gemv_kslice(int nr_max, int K) {
-    int chunks = kGemvLdsBytes / (nr_max * 144);
-    int ks = chunks * 32;
-    return ks >= K ? K : ks;
-}
+// Matrix-core path (kern_mfma.hip).  The gate/up GEMM (dual) reads the f32 input rows
+// (compact row j = input row in_rows[j], or j) and splits them into `terms` bf16 terms
+// in LDS; it writes H as terms planes [terms][rcap][I] (+ fmt 4 per-16-column partial
+// sums hp[I/64][4][rcap]) for the down GEMM, which writes Y [rcap][D] f32.  items: int4
+// records {expert, r0, nrow, 0} with nrow <= rmax (<= 16).  A workgroup of 16 waves
+// covers one item and 16 * tpw / (ks * (dual ? 2 : 1)) output tiles of 16 rows (ks = K
+// split 1, 2 or 4; tpw = tiles per wave 1 or 2, 2 only with ks 1).  Requires fmt 4/7,
+// K % 1024 == 0, K <= kDecMaxK, K / ks <= 2048 (fmt 4) or 4096 (fmt 7), O % 1024 == 0,
+// 16-byte aligned weights, 4-byte aligned scales, 16-byte aligned input rows, LDS
+// (mfma_dec_lds_bytes) <= kDecLdsBudget and staging within kDecStage* registers.
+constexpr size_t kDecLdsBudget = 163840;
+constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4096)
+constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12288)
+constexpr int kDecMaxK = 8192;
+size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int tpw);
+hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const ExpertWork *ew,
+                           const void *items, int n_items, const float *xin, const int *in_rows,
+                           const void *pin, const float *xs, void *pout, float *hp, float *out,
+                           int K, int O, int rcap, int rmax, int act, float act_a, float act_b,
+                           hipStream_t st);
 
 }  // namespace mvllm_hip

@@ -128,15 +128,16 @@ struct Ctx {
     hipStream_t last_stream = nullptr;
     hipEvent_t last_done = nullptr;  // end of the previous call (any stream)
     bool have_last = false;
-    DevBuf H, Y, Xc, Oc, miss;
+    DevBuf H, Y, Xc, Oc, miss, Ph, HP;
     HostBuf hx, ho;
     static constexpr int kSlots = 8;
     PlanSlot slots[kSlots];
     int slot_next = 0;
     // options
     int mode = 0;
-    int mfma_min_rows = 32;
     int timing = 0;
+    int dequant_path = 0;    // mvllm_hip_dequant: 0 f32 decode, 1 matrix-core bf16 decode
+    int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2 or 4
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -246,75 +247,121 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// lanes per output row: the divisor of the chunk count closest to 4 chunks per lane
-int pick_lanes(int nch) {
-    int best = 64;
-    int bestd = 1 << 30;
-    for (int L : {64, 32, 16, 8}) {
-        if (nch % L)
-            continue;
-        const int dd = std::abs(nch / L - 4);
-        if (dd < bestd) {
-            bestd = dd;
-            best = L;
-        }
-    }
-    return best;
-}
-
+// How one call runs: the matrix-core path for both projections (activation planes,
+// items of up to rmax rows), or the exact element-wise kernels.
 struct PhaseCfg {
-    bool fast;
-    int nr_max, L, passes, rows_per_tile, tiles;
+    int rmax = 0, ks = 1, tpw = 1;
+    size_t it0 = 0, it_split = 0, it1 = 0;  // item range; [it0, it_split) = experts < split
 };
 
-PhaseCfg pick_phase(int fmt, int K, int O, const Plan &P, size_t first, size_t count,
-                    bool dual, const void *in) {
-    PhaseCfg c{};
-    c.fast = (fmt == 4 || fmt == 7) && K % 32 == 0 && aligned(in, 16);
-    for (size_t i = first; c.fast && i < first + count; ++i) {
-        const ExpertWork &w = P.ew[i];
-        for (int m = dual ? 0 : 2; m < (dual ? 2 : 3); ++m)
-            c.fast = c.fast && aligned(w.w[m], 16) && (fmt == 7 || aligned(w.s[m], 4));
-    }
-    int nrm = 0;
-    for (size_t i = first; i < first + count; ++i)
-        nrm = std::max(nrm, P.ew[i].nrows);
-    c.nr_max = nrm <= 1 ? 1 : nrm <= 2 ? 2 : nrm <= 4 ? 4 : 8;
-    if (c.fast) {
-        const int ks = gemv_kslice(c.nr_max, K);
-        c.L = pick_lanes(ks / 32);
-        c.passes = 1;
-        c.rows_per_tile = gemv_rows_per_tile(c.L, 1);
-        // keep very large grids within ~16K workgroups
-        while ((size_t)count * ((O + c.rows_per_tile - 1) / c.rows_per_tile) > 16384 &&
-               c.passes < 8) {
-            c.passes *= 2;
-            c.rows_per_tile = gemv_rows_per_tile(c.L, c.passes);
+struct CallCfg {
+    bool mfma = false;
+    int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
+    PhaseCfg gu, dn;
+    std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
+};
+
+// Largest K / ks whose tile scales fit the kernel's per-lane scale registers.
+int dec_max_kr(int fmt) { return fmt == 4 ? 2048 : 4096; }
+
+bool dec_fits(int fmt, int K, int rmax, int terms, bool dual, int ks, int tpw) {
+    if (K / ks > dec_max_kr(fmt))
+        return false;
+    const size_t stage = dual ? (size_t)rmax * (K / 8)
+                              : (size_t)terms * rmax * (K / 8);
+    const size_t cap = (size_t)(dual ? kDecStageDual : kDecStageSingle) * 1024;
+    return stage <= cap && mfma_dec_lds_bytes(fmt, K, rmax, terms, dual, ks, tpw) <= kDecLdsBudget;
+}
+
+// Largest rows-per-item (<= want) that fits with some (ks, tpw); 0 if none.
+int pick_rmax(int fmt, int K, int terms, bool dual, int want) {
+    for (int r = std::min(16, want); r > 0; --r)
+        for (int ks : {1, 2, 4})
+            if (dec_fits(fmt, K, r, terms, dual, ks, 1))
+                return r;
+    return 0;
+}
+
+bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t split, int fmt,
+               int K, int O, bool dual) {
+    // LDS holds activations for the largest item actually present, within the limits
+    int most = 1;
+    for (const ExpertWork &w : P.ew)
+        most = std::max(most, w.nrows);
+    ph.rmax = pick_rmax(fmt, K, cc.terms, dual, most);
+    size_t n_items = 0;
+    for (const ExpertWork &w : P.ew)
+        n_items += (size_t)((w.nrows + ph.rmax - 1) / ph.rmax);
+    // One workgroup (16 waves) fills a CU.  Each wave streams tpw tiles x K/ks of one
+    // matrix; pick the admissible (ks, tpw) minimising rounds x per-wave blocks (+ a fixed
+    // ramp of ~4 blocks per round) over the 256 CUs.
+    const size_t tasks = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // waves at ks=tpw=1
+    const int opts[4][2] = {{1, 1}, {2, 1}, {4, 1}, {1, 2}};
+    double best = 1e30;
+    for (const auto &kt : opts) {
+        if (!dec_fits(fmt, K, ph.rmax, cc.terms, dual, kt[0], kt[1]))
+            continue;
+        if (C.dec_ks && (kt[0] != C.dec_ks || kt[1] != 1))
+            continue;
+        const size_t wgs = tasks * (size_t)kt[0] / (16 * (size_t)kt[1]);
+        const double rounds = (double)((wgs + 255) / 256);
+        const double cost = rounds * ((double)(K / 256) * kt[1] / kt[0] + 4.0);
+        if (cost < best - 1e-9) {
+            best = cost;
+            ph.ks = kt[0];
+            ph.tpw = kt[1];
         }
-    } else {
-        c.rows_per_tile = 4;
     }
-    c.tiles = (O + c.rows_per_tile - 1) / c.rows_per_tile;
-    return c;
+    if (best >= 1e30)
+        return false;
+    ph.it0 = cc.items.size() / 4;
+    ph.it_split = ph.it0;
+    for (size_t i = 0; i < P.ew.size(); ++i) {
+        if (i == split)
+            ph.it_split = cc.items.size() / 4;
+        for (int r0 = 0; r0 < P.ew[i].nrows; r0 += ph.rmax) {
+            cc.items.push_back(static_cast<int>(i));
+            cc.items.push_back(r0);
+            cc.items.push_back(std::min(ph.rmax, P.ew[i].nrows - r0));
+            cc.items.push_back(0);
+        }
+    }
+    ph.it1 = cc.items.size() / 4;
+    if (split >= P.ew.size())
+        ph.it_split = ph.it1;
+    return true;
 }
 
-hipError_t run_gemv(int fmt, bool dual, const PhaseCfg &c, GemvArgs a, hipStream_t st) {
-    a.tiles_per_expert = c.tiles;
-    a.rows_per_tile = c.rows_per_tile;
-    return c.fast ? launch_gemv_fast(fmt, dual, c.nr_max, c.L, c.passes, a, st)
-                  : launch_gemv_generic(fmt, dual, a, st);
+void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, size_t split,
+               const void *in) {
+    cc = CallCfg();
+    // bf16 terms per activation: 2 (default) represents each f32 activation to 2^-17
+    // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2)
+    cc.terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
+    bool ok = (fmt == 4 || fmt == 7) && D % 1024 == 0 && I % 1024 == 0 && D <= kDecMaxK &&
+              I <= kDecMaxK && aligned(in, 16);
+    // (% 1024 also covers the O % 512 == 0 that 16-wave workgroups of 2-tile waves need)
+    for (const ExpertWork &w : P.ew)
+        for (int m = 0; m < 3; ++m)
+            ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], 4);
+    if (!ok || pick_rmax(fmt, D, cc.terms, true, 1) < 1 || pick_rmax(fmt, I, cc.terms, false, 1) < 1)
+        return;
+    cc.mfma = add_phase(C, cc, cc.gu, P, split, fmt, D, I, true) &&
+              add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
+    if (!cc.mfma)
+        cc.items.clear();
 }
 
-// Upload the plan (experts, xrow, combine CSR) through a pinned slot; returns device
-// pointers into the slot's device buffer.
+// Upload the plan (experts, xrow, combine CSR, items) through a pinned slot; returns
+// device pointers into the slot's device buffer.
 struct DevPlan {
     ExpertWork *ew;
-    int *xrow, *tok_ptr, *ent_row, *out_row;
+    int *xrow, *tok_ptr, *ent_row, *out_row, *items;
     float *ent_w;
     PlanSlot *slot;
 };
 
-int upload_plan(Ctx &C, const Plan &P, hipStream_t st, DevPlan &dp) {
+int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp) {
     PlanSlot &s = C.slots[C.slot_next];
     C.slot_next = (C.slot_next + 1) % Ctx::kSlots;
     if (s.used)
@@ -323,8 +370,8 @@ int upload_plan(Ctx &C, const Plan &P, hipStream_t st, DevPlan &dp) {
     const size_t b_ew = al(P.ew.size() * sizeof(ExpertWork));
     const size_t b_x = al(P.xrow.size() * 4), b_tp = al(P.tok_ptr.size() * 4);
     const size_t b_er = al(P.ent_row.size() * 4), b_or = al(P.out_row.size() * 4);
-    const size_t b_ew2 = al(P.ent_w.size() * 4);
-    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2;
+    const size_t b_ew2 = al(P.ent_w.size() * 4), b_it = al(cc.items.size() * 4);
+    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it;
     HIP_TRY(s.host.ensure(total));
     HIP_TRY(s.dev.ensure(total));
     char *h = static_cast<char *>(s.host.p);
@@ -342,6 +389,7 @@ int upload_plan(Ctx &C, const Plan &P, hipStream_t st, DevPlan &dp) {
     const size_t o_er = put(P.ent_row.data(), P.ent_row.size() * 4, b_er);
     const size_t o_or = put(P.out_row.data(), P.out_row.size() * 4, b_or);
     const size_t o_w = put(P.ent_w.data(), P.ent_w.size() * 4, b_ew2);
+    const size_t o_it = put(cc.items.data(), cc.items.size() * 4, b_it);
     HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
     char *d = static_cast<char *>(s.dev.p);
     dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
@@ -350,6 +398,7 @@ int upload_plan(Ctx &C, const Plan &P, hipStream_t st, DevPlan &dp) {
     dp.ent_row = reinterpret_cast<int *>(d + o_er);
     dp.out_row = reinterpret_cast<int *>(d + o_or);
     dp.ent_w = reinterpret_cast<float *>(d + o_w);
+    dp.items = reinterpret_cast<int *>(d + o_it);
     dp.slot = &s;
     return 1;
 }
@@ -371,54 +420,83 @@ int finish_call(Ctx &C, hipStream_t st, PlanSlot *slot) {
     return 1;
 }
 
-// The three phases.  `split` experts [0, split) run gate/up first; a wait on
-// `gate_event` (may be null) precedes gate/up of [split, n).
-int run_phases(Ctx &C, const Plan &P, const DevPlan &dp, int fmt, int D, int I, int act,
-               float a, float b, const float *in, const int *in_rows, float *out,
+GemvArgs generic_args(const DevPlan &dp, size_t first, size_t count, const int *in_rows,
+                      const float *in, float *out, int K, int O, int act, float a, float b) {
+    GemvArgs g{};
+    g.ew = dp.ew + first;
+    g.n_experts = static_cast<int>(count);
+    g.in_rows = in_rows;
+    g.in = in;
+    g.out = out;
+    g.K = K;
+    g.O = O;
+    g.act = act;
+    g.act_a = a;
+    g.act_b = b;
+    g.rows_per_tile = 4;
+    g.tiles_per_expert = (O + 3) / 4;
+    return g;
+}
+
+// The phases of one call.  Experts [0, split) run gate/up first; a wait on `gate_event`
+// (may be null) precedes gate/up of [split, n).
+int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int fmt, int D,
+               int I, int act, float a, float b, const float *in, const int *in_rows, float *out,
                hipStream_t st, size_t split, hipEvent_t gate_event) {
     const size_t n = P.ew.size(), R = P.xrow.size();
-    HIP_TRY(C.H.ensure(std::max<size_t>(R * I * 4, 256)));
-    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
+    const int rcap = static_cast<int>(R);
     TimedCall tc{};
     if (C.timing) {
         for (auto &e : tc.ev)
             HIP_TRY(hipEventCreate(&e));
         HIP_TRY(hipEventRecord(tc.ev[0], st));
     }
-    GemvArgs g{};
-    g.in_rows = in_rows;
-    g.in = in;
-    g.out = static_cast<float *>(C.H.p);
-    g.K = D;
-    g.O = I;
-    g.act = act;
-    g.act_a = a;
-    g.act_b = b;
-    for (int part = 0; part < 2; ++part) {
-        const size_t first = part == 0 ? 0 : split, cnt = part == 0 ? split : n - split;
-        if (part == 1 && gate_event)
-            HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
-        if (!cnt)
-            continue;
-        g.ew = dp.ew + first;
-        g.n_experts = static_cast<int>(cnt);
-        const PhaseCfg c = pick_phase(fmt, D, I, P, first, cnt, true, in);
-        HIP_TRY(run_gemv(fmt, true, c, g, st));
-        C.stats[13] += 1;
-    }
-    if (C.timing)
-        HIP_TRY(hipEventRecord(tc.ev[1], st));
-    GemvArgs dn{};
-    dn.ew = dp.ew;
-    dn.n_experts = static_cast<int>(n);
-    dn.in_rows = nullptr;
-    dn.in = static_cast<const float *>(C.H.p);
-    dn.out = static_cast<float *>(C.Y.p);
-    dn.K = I;
-    dn.O = D;
-    {
-        const PhaseCfg c = pick_phase(fmt, I, D, P, 0, n, false, C.H.p);
-        HIP_TRY(run_gemv(fmt, false, c, dn, st));
+    if (cc.mfma) {
+        const size_t tb = (size_t)cc.terms * 2;
+        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
+        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
+        for (int part = 0; part < 2; ++part) {
+            const size_t i0 = part ? cc.gu.it_split : cc.gu.it0;
+            const size_t i1 = part ? cc.gu.it1 : cc.gu.it_split;
+            if (part == 1 && gate_event)
+                HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+            if (i1 <= i0)
+                continue;
+            HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.tpw, dp.ew,
+                                    dp.items + 4 * i0, static_cast<int>(i1 - i0), in, in_rows,
+                                    nullptr, nullptr, C.Ph.p, static_cast<float *>(C.HP.p),
+                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, st));
+            C.stats[13] += 1;
+        }
+        if (C.timing)
+            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.tpw, dp.ew,
+                                dp.items + 4 * cc.dn.it0,
+                                static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, nullptr,
+                                C.Ph.p, static_cast<const float *>(C.HP.p), nullptr, nullptr,
+                                static_cast<float *>(C.Y.p), I, D, rcap, cc.dn.rmax, 0, 0.f, 0.f,
+                                st));
+        C.stats[14] += 1;
+    } else {
+        for (int part = 0; part < 2; ++part) {
+            const size_t first = part == 0 ? 0 : split, cnt = part == 0 ? split : n - split;
+            if (part == 1 && gate_event)
+                HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+            if (!cnt)
+                continue;
+            HIP_TRY(launch_gemv_generic(fmt, true,
+                                        generic_args(dp, first, cnt, in_rows, in,
+                                                     static_cast<float *>(C.H.p), D, I, act, a, b),
+                                        st));
+            C.stats[13] += 1;
+        }
+        if (C.timing)
+            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(launch_gemv_generic(fmt, false,
+                                    generic_args(dp, 0, n, nullptr,
+                                                 static_cast<const float *>(C.H.p),
+                                                 static_cast<float *>(C.Y.p), I, D, 0, 0.f, 0.f),
+                                    st));
         C.stats[14] += 1;
     }
     if (C.timing)
@@ -543,6 +621,8 @@ void mvllm_hip_shutdown(void) {
     C.free_blocks.clear();
     C.H.release();
     C.Y.release();
+    C.Ph.release();
+    C.HP.release();
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
@@ -580,13 +660,17 @@ int mvllm_hip_set_option(const char *key, long long value) {
         return 0;
     const std::string k(key);
     if (k == "mode") {
-        if (value < 0 || value > 3)
+        if (value < 0 || value > 2)
             return 0;
         C.mode = static_cast<int>(value);
-    } else if (k == "mfma_min_rows") {
-        C.mfma_min_rows = static_cast<int>(std::max<long long>(1, value));
     } else if (k == "timing") {
         C.timing = value ? 1 : 0;
+    } else if (k == "dec_ks") {
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return 0;
+        C.dec_ks = static_cast<int>(value);
+    } else if (k == "dequant_path") {
+        C.dequant_path = value ? 1 : 0;
     } else {
         return 0;
     }
@@ -621,10 +705,15 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
         return 1;
     if (!order_after_previous(C, st))
         return 0;
+    const size_t R = P.xrow.size();
+    HIP_TRY(C.H.ensure(std::max<size_t>(R * Iinter * 4, 256)));
+    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
+    CallCfg cc;
+    plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg);
     DevPlan dp{};
-    if (!upload_plan(C, P, st, dp))
+    if (!upload_plan(C, P, cc, st, dp))
         return 0;
-    if (!run_phases(C, P, dp, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
+    if (!run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
                     P.ew.size(), nullptr))
         return 0;
     return finish_call(C, st, dp.slot);
@@ -751,10 +840,14 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     std::vector<int> dest_rows = P.out_row;
     for (size_t t = 0; t < T; ++t)
         P.out_row[t] = static_cast<int>(t);
+    HIP_TRY(C.H.ensure(std::max<size_t>(R * Iinter * 4, 256)));
+    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
+    CallCfg cc;
+    plan_call(C, cc, P, fmt, D, Iinter, hit.size(), C.Xc.p);
     DevPlan dp{};
-    if (!upload_plan(C, P, st, dp))
+    if (!upload_plan(C, P, cc, st, dp))
         return 0;
-    const int ok = run_phases(C, P, dp, fmt, D, Iinter, act, act_a, act_b,
+    const int ok = run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b,
                               static_cast<const float *>(C.Xc.p), nullptr,
                               static_cast<float *>(C.Oc.p), st, hit.size(), miss_ev);
     if (!ok)
@@ -923,7 +1016,10 @@ int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, i
         set_err("dequant: bad arguments");
         return 0;
     }
-    HIP_TRY(launch_dequant(fmt, packed_dev, scales_dev, O, K, w_dev, C.own));
+    if (C.dequant_path)
+        HIP_TRY(launch_dequant_bf16path(fmt, packed_dev, scales_dev, O, K, w_dev, C.own));
+    else
+        HIP_TRY(launch_dequant(fmt, packed_dev, scales_dev, O, K, w_dev, C.own));
     HIP_TRY(hipStreamSynchronize(C.own));
     return 1;
 }
@@ -939,6 +1035,34 @@ int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_de
     }
     HIP_TRY(launch_quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev, C.own));
     HIP_TRY(hipStreamSynchronize(C.own));
+    return 1;
+}
+
+int mvllm_hip_membench(int kind, const void *src_dev, void *dst_dev, size_t bytes, int row_bytes,
+                       int reps, double *ms_per_rep) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !src_dev || !dst_dev || bytes < 4096 || reps < 1 || kind < 0 || kind > 6 ||
+        (kind >= 2 && (row_bytes < 1024 || row_bytes % 1024))) {
+        set_err("membench: bad arguments");
+        return 0;
+    }
+    hipEvent_t e0, e1;
+    HIP_TRY(hipEventCreate(&e0));
+    HIP_TRY(hipEventCreate(&e1));
+    HIP_TRY(launch_membench(kind, src_dev, dst_dev, bytes, row_bytes / 16, C.own));  // warm-up
+    HIP_TRY(hipEventRecord(e0, C.own));
+    for (int r = 0; r < reps; ++r)
+        HIP_TRY(launch_membench(kind, src_dev, dst_dev, bytes, row_bytes / 16, C.own));
+    HIP_TRY(hipEventRecord(e1, C.own));
+    HIP_TRY(hipEventSynchronize(e1));
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (ms_per_rep)
+        *ms_per_rep = ms / reps;
     return 1;
 }
 

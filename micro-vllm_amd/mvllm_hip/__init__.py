@@ -56,6 +56,7 @@ _SIGS = {
     "mvllm_hip_stats_reset": (None, []),
     "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
     "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
+    "mvllm_hip_membench": (_i, [_i, _p, _p, _sz, _i, _i, _p]),
 }
 
 _lib = None
@@ -129,11 +130,18 @@ def moe_block(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, o
     return rc
 
 
+def prepare_lists(g, u, d, gs, us, ds):
+    """Pointer lists -> ctypes arrays, reusable across moe_block_dev calls."""
+    return tuple(None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds))
+
+
 def moe_block_dev(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
-                  act=ACT_SILU, act_a=0.0, act_b=0.0, stream=None, check=True):
+                  act=ACT_SILU, act_a=0.0, act_b=0.0, stream=None, check=True, prepared=None):
     """Device variant: g..ds are lists of device pointers (ints) or torch tensors;
-    xg/out are torch CUDA tensors; xoff/nr/rows/rw are numpy host arrays."""
-    pa = [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
+    xg/out are torch CUDA tensors; xoff/nr/rows/rw are numpy host arrays.
+    `prepared` (from prepare_lists) replaces g..ds when given."""
+    pa = prepared if prepared is not None else \
+        [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
     st = None if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
     rc = lib().mvllm_hip_moe_block_dev(nb, D, Iinter, fmt, 0, *pa, _ptr(xg), _ptr(xoff),
                                        _ptr(nr), _ptr(rows), _ptr(rw), _ptr(out), S, act, act_a,
@@ -203,3 +211,11 @@ def dequant(fmt, packed_dev, scales_dev, O, K, w_dev):
 def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):
     _check(lib().mvllm_hip_quantize_mxfp4(_ptr(x_dev), n, K, _ptr(codes_dev), _ptr(scales_dev)),
            "mvllm_hip_quantize_mxfp4")
+
+
+def membench(kind, src, dst, nbytes, row_bytes=0, reps=5):
+    """-> ms per repetition of the memory probe (see mvllm_hip_membench)."""
+    ms = np.zeros(1, np.float64)
+    _check(lib().mvllm_hip_membench(kind, _ptr(src), _ptr(dst), nbytes, row_bytes, reps,
+                                    _ptr(ms)), "mvllm_hip_membench")
+    return float(ms[0])

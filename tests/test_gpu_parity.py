@@ -87,6 +87,32 @@ def test_dequant_bit_exact(hip, orc, fmt, O, K, offset):
     assert np.array_equal(got[m].view(np.uint32), exp[m].view(np.uint32))
 
 
+@pytest.mark.parametrize("fmt,O,K", [(4, 48, 2048), (4, 16, 1024), (7, 48, 7168), (7, 16, 1024)])
+def test_dequant_bit_exact_mfma_decode(hip, orc, fmt, O, K):
+    """The weights exactly as the matrix-core path decodes them (bf16 operands), checked
+    bit for bit, including zero/infinite ue8m0 scale bytes."""
+    say("dequant mfma path", fmt, O, K)
+    rng = np.random.default_rng(O + K + 7 * fmt)
+    packed = rng.integers(0, 256, size=(O, K // 2), dtype=np.uint8)
+    if fmt == 4:
+        scales = rng.uniform(-0.03, 0.03, size=(O, K // 64)).astype(np.float32)
+    else:
+        scales = rng.integers(1, 255, size=(O, K // 32), dtype=np.uint8)
+        scales[0, :4] = [0, 255, 1, 254]
+    w = torch.empty((O, K), dtype=torch.float32, device="cuda")
+    assert hip.set_option("dequant_path", 1)
+    try:
+        hip.dequant(fmt, dev(packed), dev(scales), O, K, w)
+    finally:
+        hip.set_option("dequant_path", 0)
+    got = w.cpu().numpy()
+    exp = orc.dequant(fmt, packed, scales, O, K)
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+    m = ~np.isnan(exp)
+    bad = np.argwhere(got[m].view(np.uint32) != exp[m].view(np.uint32))
+    assert bad.size == 0, (got[m][bad[:5, 0]], exp[m][bad[:5, 0]])
+
+
 def test_quantize_mxfp4_bit_exact(hip, orc):
     say("quantize_mxfp4")
     rng = np.random.default_rng(77)
@@ -122,7 +148,27 @@ DEV_CASES = [
     (7, 1024, 512, [3, 1, 2, 6], 6, 2, 4.0, 25.0, (), 1),
     (7, 65, 31, [1, 1], 2, 2, 4.0, 25.0, (), 0),
     (0, 64, 48, [2, 1], 3, 1, 3.0, 0.0, (0,), 0),                  # f32 weights
+    (4, 2048, 1024, [7, 1, 13], 16, 1, 7.0, 0.0, (), 0),           # rows > one item
+    (7, 2048, 1024, [5, 9], 12, 2, 4.0, 25.0, (), 0),
 ]
+
+
+@pytest.mark.parametrize("case", [DEV_CASES[1], DEV_CASES[7], DEV_CASES[-2]])
+def test_moe_block_bf16_mode(hip, orc, case):
+    """mode 2: activations rounded to bf16 (one term) -- the north-star tolerance 1e-2."""
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("bf16 mode", case)
+    rng = np.random.default_rng(D * 3 + I)
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    assert hip.set_option("mode", 2)
+    try:
+        got = run_dev(hip, c, act, a, b)
+    finally:
+        hip.set_option("mode", 0)
+    exp = oracle_out(orc, c, act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < 1e-2
 
 
 @pytest.mark.parametrize("case", DEV_CASES)
