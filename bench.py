@@ -152,6 +152,13 @@ def main():
     dn_gbs = w.nb * b_dn / (ms_dn * 1e-3) / 1e9
     log(f"gate/up {gu_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s")
 
+    # achievable HBM streaming-read rate on this box: coalesced 16-byte loads over the
+    # whole pool (>= 4 GiB, beyond the Infinity Cache), after one warm-up pass
+    sink = torch.zeros(4096, dtype=torch.uint8, device="cuda")
+    probe_bytes = (pool.numel() // 4096) * 4096
+    hbm_gbs = probe_bytes / mvllm_hip.membench(0, pool, sink, probe_bytes, 0, 5) / 1e6
+    log(f"HBM stream-read probe: {hbm_gbs:.0f} GB/s over {probe_bytes / 2**30:.2f} GiB")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, args.cpu_seconds)
@@ -174,6 +181,7 @@ def main():
                    "topk": k, "T": T, "fmt": fmt, "experts_per_step": int(w.nb),
                    "rows": int(w.nr.sum()), "mode": args.mode},
         "weight_gbps": round(wbytes / ms_step / 1e6, 1),
+        "hbm_probe_gbps": round(hbm_gbs, 1),
         "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": None,
