@@ -18,120 +18,13 @@
 // column t take K elements [8q, 8q+8) of the 32-wide step; C[4q + i][t], i = 0..3.
 // Within a 64-wide group, step s in {0,1} takes K offsets 16q + 8s .. +8, so a lane's
 // 16 weights of the group are 8 contiguous bytes and one scale serves the whole chain.
-#include "moe_internal.h"
+#include "mfma_common.h"
 
 #include <algorithm>
 #include <cmath>
 
 namespace mvllm_hip {
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f4v __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float mf_sigmoid(float x) {
-    if (x >= 0.f)
-        return 1.f / (1.f + expf(-x));
-    const float z = expf(x);
-    return z / (1.f + z);
-}
-
-__device__ __forceinline__ float mf_act(int act, float g, float u, float a, float b) {
-    if (act == ACT_CLAMP_SWIGLU) {
-        if (a > 0.f && g > a)
-            g = a;
-        const float s = g * mf_sigmoid(g);
-        if (a > 0.f)
-            u = fminf(fmaxf(u, -a), a);
-        return s * u;
-    }
-    if (act == ACT_SITU)
-        return a * tanhf(g / a) * mf_sigmoid(g) * b * tanhf(u / b);
-    return g * mf_sigmoid(g) * u;
-}
-
-__device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) {
-    bf16x8 r;
-    r[0] = a[0]; r[1] = a[1]; r[2] = b[0]; r[3] = b[1];
-    r[4] = c[0]; r[5] = c[1]; r[6] = d[0]; r[7] = d[1];
-    return r;
-}
-
-__device__ __forceinline__ float mf_mx4_lut(uint32_t n) {
-    const uint32_t e = (n >> 1) & 3u, m = n & 1u;
-    const float mag = e == 0 ? 0.5f * (float)m : (1.f + 0.5f * (float)m) * (float)(1u << (e - 1));
-    return (n & 8u) ? -mag : mag;
-}
-
-// MXFP4 weights whose scale byte e would take lut[n] * 2^(e-127) out of bf16's normal
-// range (e < 2 or e > 252; the reference's e = 0 means +0 and e = 255 means +inf):
-// form the product in f32 as the reference does; it is exactly representable in bf16
-// (or is +-0 / +-inf / NaN), so its high half is the operand.
-__device__ __forceinline__ bf16x8 decode_b7_exact(uint32_t w, float scale7) {
-    bf16x8 r;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float f = mf_mx4_lut((w >> (4 * k)) & 15u) * scale7;
-        r[k] = __builtin_bit_cast(__bf16, (unsigned short)(__float_as_uint(f) >> 16));
-    }
-    return r;
-}
-
-// One dword = 8 weights (K order e0..e7) of one step -> B operand.
-// fmt 4 yields slot order [e0 e2 e4 e6 e1 e3 e5 e7] (the A side is stored permuted to
-// match); fmt 7 yields natural order with the block scale folded in, exact for scale
-// bytes 2..252 (callers patch the others with decode_b7_exact, see b7_exceptional).
-template <int FMT>
-__device__ __forceinline__ bf16x8 decode_b(uint32_t w, float scale7) {
-    if constexpr (FMT == 4) {
-        const int lo = (int)(w & 0x0F0F0F0Fu), hi = (int)((w >> 4) & 0x0F0F0F0Fu);
-        return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, false),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, true),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, false),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, true));
-    } else {
-        return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 0),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 1),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 2),
-                     __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 3));
-    }
-}
-
-// Scale bytes the converter does not reproduce: e = 0 (+0 in the reference, 2^-127 in
-// hardware), e = 1 (subnormal products) and e > 252 (overflow; e = 255 is +inf).
-__device__ __forceinline__ bool b7_exceptional(float scale7) {
-    const uint32_t e = __float_as_uint(scale7) >> 23;
-    return e < 2u || e > 252u;
-}
-
-// Position of K element e (within its 8-block) in the stored A row.
-template <int FMT>
-__device__ __forceinline__ int a_slot(int e) {
-    if constexpr (FMT == 4)
-        return (e & 1) ? 4 + (e >> 1) : (e >> 1);
-    else
-        return e;
-}
-
-// f32 -> TERMS bf16 terms (hi, then successive remainders); returns the f32 value the
-// terms represent (what the MFMA actually multiplies).
-template <int TERMS>
-__device__ __forceinline__ float split_terms(float x, __bf16 (&t)[3]) {
-    t[0] = (__bf16)x;
-    float rep = (float)t[0];
-    if constexpr (TERMS >= 2) {
-        const float r1 = x - rep;
-        t[1] = (__bf16)r1;
-        rep += (float)t[1];
-        if constexpr (TERMS >= 3) {
-            const float r2 = r1 - (float)t[1];
-            t[2] = (__bf16)r2;
-            rep += (float)t[2];
-        }
-    }
-    return rep;
-}
 
 // ---------------------------------------------------------------------------------
 // Activation planes.  A GEMM input row is held as TERMS bf16 planes P[tm][j][K] (fmt 4:
@@ -185,13 +78,6 @@ struct DecArgs {
 constexpr int kDecThreads = 1024;
 constexpr int kScaleDw = 8;  // scale dwords per lane and tile (<= 128 scale bytes per row)
 
-// Raw buffer resource over [p, p + bytes) (gfx9 descriptor: stride 0, word 3 = 0x20000).
-// Loads through it take a per-lane 32-bit offset plus a wave-uniform offset; offsets past
-// `bytes` read as 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void *p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)bytes,
-                                             0x00020000);
-}
 
 // Weights of one 256-wide K block of a tile, as loaded (lane l: row l / 4).
 struct WBlock {

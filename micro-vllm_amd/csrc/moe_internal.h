@@ -80,4 +80,22 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const
                            int K, int O, int rcap, int rmax, int act, float act_a, float act_b,
                            hipStream_t st);
 
+// Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
+// nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per
+// (item, block of 128 columns of each of gate/up, or 256 columns of down).  Requires
+// fmt 4/7, K % 256 == 0, O % 128 (dual) / % 256 (single) == 0, 8-byte aligned weights,
+// 16-byte (int4) / 8-byte (MXFP4) aligned scales and 16-byte aligned planes.  Inputs are
+// the plane format of the decode kernel: [terms][rcap][K] bf16 (+ int4 sums
+// [K/64][4][rcap]); launch_prep_planes builds them from f32 rows.
+// Largest row-tile count per workgroup that compiles without spills: int4 carries a
+// per-group chain and scale per row tile, so it stops at 2 tiles (32 rows).
+inline int gemm_max_mt(int fmt, int terms) { return fmt == 4 ? 2 : terms == 1 ? 8 : 4; }
+size_t gemm_lds_bytes(int fmt, int terms, int mt);
+hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
+                       const void *items, int n_items, const void *pin, const float *xs,
+                       void *pout, float *hp, float *out, int K, int O, int rcap, int act,
+                       float act_a, float act_b, hipStream_t st);
+hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
+                              int K, int rcap, void *planes, float *xs, hipStream_t st);
+
 }  // namespace mvllm_hip

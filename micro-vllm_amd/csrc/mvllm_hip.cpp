@@ -128,7 +128,7 @@ struct Ctx {
     hipStream_t last_stream = nullptr;
     hipEvent_t last_done = nullptr;  // end of the previous call (any stream)
     bool have_last = false;
-    DevBuf H, Y, Xc, Oc, miss, Ph, HP;
+    DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp, XS;
     HostBuf hx, ho;
     static constexpr int kSlots = 8;
     PlanSlot slots[kSlots];
@@ -138,6 +138,7 @@ struct Ctx {
     int timing = 0;
     int dequant_path = 0;    // mvllm_hip_dequant: 0 f32 decode, 1 matrix-core bf16 decode
     int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2 or 4
+    int gemm = 0;            // grouped GEMM: 0 auto, 1 whenever it applies, 2 never
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -254,11 +255,21 @@ struct PhaseCfg {
     size_t it0 = 0, it_split = 0, it1 = 0;  // item range; [it0, it_split) = experts < split
 };
 
+// Row-block class of the grouped GEMM: items of 16 * mt rows at most, in
+// [it0, it1) of CallCfg::items; items of experts < split come first, up to it_split.
+struct GemmCls {
+    int mt = 0;
+    size_t it0 = 0, it_split = 0, it1 = 0;
+};
+
 struct CallCfg {
-    bool mfma = false;
+    bool mfma = false;        // decode-shaped matrix-core kernels
+    bool gemm = false;        // grouped GEMM (prefill-shaped)
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
+    GemmCls gcls[4];
+    int n_gcls = 0;
 };
 
 // Largest K / ks whose tile scales fit the kernel's per-lane scale registers.
@@ -332,24 +343,81 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
     return true;
 }
 
+// Grouped-GEMM items: each expert's rows in blocks of 16 * max_mt, the remainder in the
+// smallest class that holds it; classes ordered by mt, experts ascending within each.
+void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
+    cc.terms = cc.terms >= 2 ? 2 : 1;
+    const int max_mt = gemm_max_mt(fmt, cc.terms);
+    const int bm = 16 * max_mt;
+    std::vector<int> per[4];  // class index = log2(mt)
+    size_t split_at[4] = {0, 0, 0, 0};
+    for (size_t i = 0; i < P.ew.size(); ++i) {
+        if (i == split)
+            for (int c = 0; c < 4; ++c)
+                split_at[c] = per[c].size();
+        const int n = P.ew[i].nrows;
+        for (int r0 = 0; r0 < n; r0 += bm) {
+            const int nrow = std::min(bm, n - r0);
+            const int mt = nrow <= 16 ? 1 : nrow <= 32 ? 2 : nrow <= 64 ? 4 : 8;
+            const int c = mt == 1 ? 0 : mt == 2 ? 1 : mt == 4 ? 2 : 3;
+            per[c].insert(per[c].end(), {static_cast<int>(i), r0, nrow, 0});
+        }
+    }
+    if (split >= P.ew.size())
+        for (int c = 0; c < 4; ++c)
+            split_at[c] = per[c].size();
+    cc.items.clear();
+    cc.n_gcls = 0;
+    for (int c = 0; c < 4; ++c) {
+        if (per[c].empty())
+            continue;
+        GemmCls &g = cc.gcls[cc.n_gcls++];
+        g.mt = 1 << c;
+        g.it0 = cc.items.size() / 4;
+        g.it_split = g.it0 + split_at[c] / 4;
+        cc.items.insert(cc.items.end(), per[c].begin(), per[c].end());
+        g.it1 = cc.items.size() / 4;
+    }
+    cc.gemm = true;
+}
+
 void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, size_t split,
                const void *in) {
     cc = CallCfg();
     // bf16 terms per activation: 2 (default) represents each f32 activation to 2^-17
-    // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2)
+    // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2).  The grouped GEMM takes
+    // 1 term by default (bf16 activations, the prefill arithmetic) and 2 in mode 1.
     cc.terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
     bool ok = (fmt == 4 || fmt == 7) && D % 1024 == 0 && I % 1024 == 0 && D <= kDecMaxK &&
               I <= kDecMaxK && aligned(in, 16);
     // (% 1024 also covers the O % 512 == 0 that 16-wave workgroups of 2-tile waves need)
-    for (const ExpertWork &w : P.ew)
-        for (int m = 0; m < 3; ++m)
+    bool gok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && aligned(in, 16);
+    int most = 0;
+    for (const ExpertWork &w : P.ew) {
+        most = std::max(most, w.nrows);
+        for (int m = 0; m < 3; ++m) {
             ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], 4);
-    if (!ok || pick_rmax(fmt, D, cc.terms, true, 1) < 1 || pick_rmax(fmt, I, cc.terms, false, 1) < 1)
+            gok = gok && aligned(w.w[m], 8) && aligned(w.s[m], fmt == 4 ? 16 : 8);
+        }
+    }
+    // grouped GEMM when forced, or when some expert has more rows than one decode item
+    if (gok && C.gemm != 2 && (C.gemm == 1 || most > 16)) {
+        cc.terms = C.mode == 1 ? 2 : 1;
+        plan_gemm(cc, P, split, fmt);
         return;
-    cc.mfma = add_phase(C, cc, cc.gu, P, split, fmt, D, I, true) &&
-              add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
-    if (!cc.mfma)
+    }
+    if (ok && pick_rmax(fmt, D, cc.terms, true, 1) >= 1 &&
+        pick_rmax(fmt, I, cc.terms, false, 1) >= 1) {
+        cc.mfma = add_phase(C, cc, cc.gu, P, split, fmt, D, I, true) &&
+                  add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
+        if (cc.mfma)
+            return;
         cc.items.clear();
+    }
+    if (gok && C.gemm != 2) {  // decode-shaped call the decode kernels do not fit: keep
+        cc.terms = C.mode == 2 ? 1 : 2;  // the decode accuracy (2 terms) unless mode 2
+        plan_gemm(cc, P, split, fmt);
+    }
 }
 
 // Upload the plan (experts, xrow, combine CSR, items) through a pinned slot; returns
@@ -451,7 +519,38 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             HIP_TRY(hipEventCreate(&e));
         HIP_TRY(hipEventRecord(tc.ev[0], st));
     }
-    if (cc.mfma) {
+    if (cc.gemm) {
+        const size_t tb = (size_t)cc.terms * 2;
+        HIP_TRY(C.Xp.ensure(std::max<size_t>(tb * R * D, 256)));
+        HIP_TRY(C.XS.ensure(std::max<size_t>((size_t)(D / 64) * 4 * R * 4, 256)));
+        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
+        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
+        float *xs = static_cast<float *>(C.XS.p), *hp = static_cast<float *>(C.HP.p);
+        HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, C.Xp.p, xs, st));
+        for (int part = 0; part < 2; ++part) {
+            if (part == 1 && gate_event)
+                HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+            for (int c = 0; c < cc.n_gcls; ++c) {
+                const GemmCls &g = cc.gcls[c];
+                const size_t i0 = part ? g.it_split : g.it0, i1 = part ? g.it1 : g.it_split;
+                if (i1 <= i0)
+                    continue;
+                HIP_TRY(launch_gemm(fmt, true, cc.terms, g.mt, dp.ew, dp.items + 4 * i0,
+                                    static_cast<int>(i1 - i0), C.Xp.p, xs, C.Ph.p, hp, nullptr,
+                                    D, I, rcap, act, a, b, st));
+                C.stats[13] += 1;
+            }
+        }
+        if (C.timing)
+            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        for (int c = 0; c < cc.n_gcls; ++c) {
+            const GemmCls &g = cc.gcls[c];
+            HIP_TRY(launch_gemm(fmt, false, cc.terms, g.mt, dp.ew, dp.items + 4 * g.it0,
+                                static_cast<int>(g.it1 - g.it0), C.Ph.p, hp, nullptr, nullptr,
+                                static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
+            C.stats[14] += 1;
+        }
+    } else if (cc.mfma) {
         const size_t tb = (size_t)cc.terms * 2;
         HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
         HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
@@ -623,6 +722,8 @@ void mvllm_hip_shutdown(void) {
     C.Y.release();
     C.Ph.release();
     C.HP.release();
+    C.Xp.release();
+    C.XS.release();
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
@@ -669,6 +770,10 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return 0;
         C.dec_ks = static_cast<int>(value);
+    } else if (k == "gemm") {
+        if (value < 0 || value > 2)
+            return 0;
+        C.gemm = static_cast<int>(value);
     } else if (k == "dequant_path") {
         C.dequant_path = value ? 1 : 0;
     } else {

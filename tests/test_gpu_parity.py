@@ -353,3 +353,86 @@ def test_two_streams_in_sequence(hip, orc):
     torch.cuda.synchronize()
     assert npref.rel_err(o1.cpu().numpy(), oracle_out(orc, c1, 1, 7.0, 0.0)) < TOL_F32
     assert npref.rel_err(o2.cpu().numpy(), oracle_out(orc, c2, 2, 4.0, 25.0)) < TOL_F32
+
+
+# ------------------------------------------------------------- grouped GEMM (prefill)
+
+TOL_BF16 = 1e-2   # one bf16 term per activation (the prefill arithmetic)
+TOL_2TERM = 5e-5  # two bf16 terms per activation (mode 1)
+
+GEMM_CASES = [
+    # fmt, D, I, nr, S, act, a, b, null_experts, invalid_rows
+    (4, 1024, 512, [40, 17, 3, 70, 1], 64, 1, 7.0, 0.0, (), 0),   # row classes 1/2, 2-3 blocks
+    (4, 256, 256, [16, 33], 40, 0, 0.0, 0.0, (), 0),              # one K step
+    (4, 512, 256, [20, 5, 9], 30, 1, 7.0, 0.0, (1,), 3),          # skips + invalid rows
+    (7, 1024, 512, [200, 5, 33, 64, 129], 256, 2, 4.0, 25.0, (), 0),  # classes 1/2/4/8
+    (7, 512, 768, [18, 140], 160, 2, 4.0, 25.0, (0,), 2),
+    (7, 256, 256, [1, 2, 3], 6, 0, 0.0, 0.0, (), 0),
+]
+
+
+def _gemm_run(hip, c, mode, gemm=1):
+    assert hip.set_option("gemm", gemm) and hip.set_option("mode", mode)
+    try:
+        return run_dev(hip, c, c.act, c.a, c.b)
+    finally:
+        hip.set_option("gemm", 0)
+        hip.set_option("mode", 0)
+
+
+@pytest.mark.parametrize("case", GEMM_CASES)
+@pytest.mark.parametrize("mode,tol", [(0, TOL_BF16), (1, TOL_2TERM)])
+def test_gemm_parity(hip, case, mode, tol):
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("gemm", mode, case)
+    rng = np.random.default_rng(D * 17 + I + sum(nr))
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    got = _gemm_run(hip, c, mode)
+    exp = npref.moe_block64(*c.args(), act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < tol
+    # rows that receive nothing are untouched
+    touched = set(int(r) for r in c.rows if 0 <= r < c.S)
+    for t in range(c.out.shape[0]):
+        if t not in touched:
+            assert np.array_equal(got[t], c.out[t])
+
+
+@pytest.mark.parametrize("fmt,D,I,nr,act,a,b", [
+    (4, 6144, 2048, [40, 21, 1], 1, 7.0, 0.0),          # c3 shapes
+    (7, 7168, 2048, [130, 3, 17], 2, 4.0, 25.0),         # c4 shapes, a full 128-row block
+])
+def test_gemm_real_shapes(hip, fmt, D, I, nr, act, a, b):
+    """Full-size prefill expert shapes; the grouped GEMM is picked automatically
+    (some expert has more than 16 rows)."""
+    say("gemm real", fmt, D, I, nr)
+    rng = np.random.default_rng(D + I + fmt)
+    c = random_case(rng, fmt, D, I, nr, 64, act, a, b)
+    got = run_dev(hip, c, act, a, b)
+    exp = npref.moe_block64(*c.args(), act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < TOL_BF16
+
+
+@pytest.mark.parametrize("name,T", [("c3", 16), ("c4", 8)])
+def test_prefill_config_parity(hip, orc, name, T):
+    """Prefill configurations at a token count the oracle finishes in seconds, through the
+    grouped GEMM, against the reference restatement."""
+    from mvllm_hip import synth
+    from cases import Case
+    say("prefill config", name, T)
+    w = synth.make_workload(name, T=T)
+    g, u, d, gs, us, ds = w.lists()
+    out = np.zeros((T, w.D), np.float32)
+    exp = out.copy()
+    assert orc.moe_block(w.nb, w.D, w.I, w.fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows,
+                         w.rw, exp, T, w.act, w.a, w.b) == 1
+    c = Case(w.nb, w.D, w.I, w.fmt, g, u, d, gs, us, ds, w.xg, w.xoff, w.nr, w.rows, w.rw, out,
+             T, w.act, w.a, w.b)
+    for mode, tol in ((0, TOL_BF16), (1, TOL_2TERM)):
+        got = _gemm_run(hip, c, mode)
+        err = npref.rel_err(got, exp)
+        say("  mode", mode, "rel_err", err)
+        assert err < tol
