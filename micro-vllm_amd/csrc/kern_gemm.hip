@@ -69,6 +69,7 @@ struct GStep {
 template <int FMT, bool DUAL, int TERMS, int MT>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     constexpr int BM = 16 * MT;
+    constexpr int PA = MT >= 8 ? 1 : 2;  // activation prefetch distance in K steps
     constexpr int PL = BM * kGemmPitch;                  // bytes per plane per stage
     constexpr int STAGE = gemm_stage_bytes(FMT, TERMS, MT);
     constexpr int ACH = TERMS * BM * (kGemmBK / 8) / kGemmThreads;  // 16-byte chunks/thread
@@ -99,7 +100,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         vw[m] = (uint32_t)(trow + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
         vs[m] = (uint32_t)(trow + t) * srow;
     }
-    auto load_b = [&](GStep<FMT> &b, int k) {
+    auto load_b = [&] __attribute__((always_inline)) (GStep<FMT> &b, int k) {
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
@@ -119,43 +120,48 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     };
 
     // A staging: chunk c = u * 512 + tid -> plane c / (BM * 32), row (c / 32) % BM,
-    // 16-byte column c % 32 of the step
-    uint4 ra[ACH];
-    float rsum = 0.f;
-    auto load_a = [&](int k) {
+    // 16-byte column c % 32 of the step.  Two register sets let the loads of step k + 2
+    // be issued while step k computes (PA = 2), so their latency spans two steps.
+    struct AStage {
+        u32x4 v[ACH];  // native vectors: copies of HIP's uint4 struct go through scratch
+        float p[4];  // int4: the four partial sums of this thread's (group, row)
+    };
+    auto load_a = [&] __attribute__((always_inline)) (AStage &ra, int k) {
+        // unconditional loads (rows past nrow re-read the last row; their results are
+        // never stored) keep the loop body free of branches
 #pragma unroll
         for (int u = 0; u < ACH; ++u) {
             const int c = u * kGemmThreads + tid;
-            const int tm = c / (BM * 32), r = (c >> 5) % BM, cc = c & 31;
-            if (r < nrow)
-                ra[u] = *reinterpret_cast<const uint4 *>(
-                    A.pin + ((size_t)tm * rcap + jbase + r) * (size_t)K + (size_t)k * kGemmBK +
-                    8 * cc);
+            const int tm = c / (BM * 32), r = min((c >> 5) % BM, nrow - 1), cc = c & 31;
+            ra.v[u] = *reinterpret_cast<const u32x4 *>(
+                A.pin + ((size_t)tm * rcap + jbase + r) * (size_t)K + (size_t)k * kGemmBK +
+                8 * cc);
         }
         if constexpr (FMT == 4) {
-            if (tid < 4 * BM) {
-                const int g = tid / BM, r = tid - g * BM;
-                if (r < nrow) {
-                    const float *p = A.xs + (size_t)(4 * k + g) * 4 * rcap + jbase + r;
-                    rsum = -8.f * (((p[0] + p[rcap]) + p[2 * rcap]) + p[3 * rcap]);
-                }
-            }
+            // the four partial sums of (group, row) are added only when stored: adding
+            // here would wait for these loads, and with them for every load issued
+            // before (loads complete in order)
+            const int i4 = tid < 4 * BM ? tid : 0;
+            const int g = i4 / BM, r = min(i4 - g * BM, nrow - 1);
+            const float *p = A.xs + (size_t)(4 * k + g) * 4 * rcap + jbase + r;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                ra.p[i] = p[i * rcap];
         }
     };
-    auto store_a = [&](int buf) {
+    auto store_a = [&] __attribute__((always_inline)) (const AStage &ra, int buf) {
         char *base = smem + buf * STAGE;
 #pragma unroll
         for (int u = 0; u < ACH; ++u) {
             const int c = u * kGemmThreads + tid;
             const int tm = c / (BM * 32), r = (c >> 5) % BM, cc = c & 31;
-            if (r < nrow)
-                *reinterpret_cast<uint4 *>(base + tm * PL + r * kGemmPitch + cc * 16) = ra[u];
+            *reinterpret_cast<u32x4 *>(base + tm * PL + r * kGemmPitch + cc * 16) = ra.v[u];
         }
         if constexpr (FMT == 4) {
             if (tid < 4 * BM) {
                 const int g = tid / BM, r = tid - g * BM;
-                if (r < nrow)
-                    reinterpret_cast<float *>(base + TERMS * PL)[g * BM + r] = rsum;
+                reinterpret_cast<float *>(base + TERMS * PL)[g * BM + r] =
+                    -8.f * (((ra.p[0] + ra.p[1]) + ra.p[2]) + ra.p[3]);
             }
         }
     };
@@ -166,7 +172,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
     const int src4 = 4 * (4 * t + q);  // ds_bpermute address of lane 4 t + q
 
-    auto compute = [&](const GStep<FMT> &b, int buf) {
+    auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf) {
         const char *base = smem + buf * STAGE;
         const float *lsum = reinterpret_cast<const float *>(base + TERMS * PL);
 #pragma unroll
@@ -236,33 +242,45 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         }
     };
 
-    // software pipeline: B two steps ahead in registers, A one step ahead in LDS
+    // software pipeline: B two steps ahead in registers; A staged into LDS one step
+    // ahead from registers loaded PA steps ahead (PA = 1 for the compute-bound 128-row
+    // class, whose registers are full).  Loads past the last step are harmless and never
+    // consumed (weights: the next rows' bytes or zeros past the buffer; activations: the
+    // step index is clamped), so the body has no branches around its loads; the
+    // scheduling barriers keep each step's uses of a register set ahead of the loads
+    // that refill it (no copies of in-flight registers, no early waits).
     const int nk = K / kGemmBK;
     GStep<FMT> b0, b1;
-    load_a(0);
+    AStage ra0, ra1;
+    load_a(ra0, 0);
+    if constexpr (PA == 2)
+        load_a(ra1, min(1, nk - 1));
     load_b(b0, 0);
-    if (nk > 1)
-        load_b(b1, 1);
-    store_a(0);
+    load_b(b1, 1);
+    store_a(ra0, 0);
     __syncthreads();
     for (int k = 0; k < nk; k += 2) {
-        if (k + 1 < nk)
-            load_a(k + 1);
+        // even step: LDS buffer 0, weights b0; stage A(k + 1) into buffer 1
+        if constexpr (PA == 2)
+            load_a(ra0, min(k + 2, nk - 1));
+        else
+            load_a(ra1, min(k + 1, nk - 1));
         compute(b0, 0);
-        if (k + 2 < nk)
-            load_b(b0, k + 2);
-        if (k + 1 < nk)
-            store_a(1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b0, k + 2);
+        store_a(ra1, 1);
         __syncthreads();
         if (k + 1 >= nk)
             break;
-        if (k + 2 < nk)
-            load_a(k + 2);
+        // odd step: LDS buffer 1, weights b1; stage A(k + 2) into buffer 0
+        if constexpr (PA == 2)
+            load_a(ra1, min(k + 3, nk - 1));
+        else
+            load_a(ra0, min(k + 2, nk - 1));
         compute(b1, 1);
-        if (k + 3 < nk)
-            load_b(b1, k + 3);
-        if (k + 2 < nk)
-            store_a(0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b1, k + 3);
+        store_a(ra0, 0);
         __syncthreads();
     }
 
