@@ -59,6 +59,8 @@ def main():
     ap.add_argument("--config", default="c1")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--mode", type=int, default=0)
+    ap.add_argument("--fp4act", action="store_true",
+                    help="MXFP4 experts: quantize activations, native scaled-FP4 matrix cores")
     ap.add_argument("--pool-gb", type=float, default=4.5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -80,6 +82,7 @@ def main():
     D, I, E, k, fmt = cfg["D"], cfg["I"], cfg["E"], cfg["k"], cfg["fmt"]
     mvllm_hip.init(0)
     mvllm_hip.set_option("mode", args.mode)
+    mvllm_hip.set_option("fp4act", 1 if args.fp4act else 0)
 
     w = synth.make_workload(args.config, T=T, with_experts=False)
     nbytes, _ = mvllm_hip.expert_geom(fmt, D, I)
@@ -139,6 +142,15 @@ def main():
     ms_dn = st["ms_down"] / args.steps
     ms_cb = st["ms_combine"] / args.steps
 
+    # arithmetic of the path the library picks (mvllm_hip.cpp plan_call): native FP4 when
+    # asked for; bf16 activations in the grouped GEMM (some expert > 16 rows); otherwise
+    # the decode kernels' f32 split into two bf16 terms
+    if args.fp4act and fmt == 7:
+        dtype = "mxfp4"
+    elif int(w.nr.max()) > 16:
+        dtype = "bf16" if args.mode != 1 else "bf16x2"
+    else:
+        dtype = {0: "bf16x2", 1: "bf16x3", 2: "bf16"}[args.mode]
     gq, sb = (64, 4) if fmt == 4 else (32, 1)
     b_gu = 2 * (I * (D // 2) + I * ((D + gq - 1) // gq) * sb)   # gate + up, one expert
     b_dn = D * (I // 2) + D * ((I + gq - 1) // gq) * sb          # down, one expert
@@ -174,15 +186,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": dtype,
         "data": "synthetic (seeded; weights random in the reference layouts, in a "
                 f"{n_blobs * nbytes / 2**30:.1f} GiB pool rotated per step)",
         "config": {"workload": f"{args.config} {cfg['desc']}, T={T}", "D": D, "I": I, "E": E,
                    "topk": k, "T": T, "fmt": fmt, "experts_per_step": int(w.nb),
-                   "rows": int(w.nr.sum()), "mode": args.mode},
+                   "rows": int(w.nr.sum()), "mode": args.mode, "fp4act": bool(args.fp4act)},
         "weight_gbps": round(wbytes / ms_step / 1e6, 1),
         "hbm_probe_gbps": round(hbm_gbs, 1),
-        "mfma_util_bf16": round(flops / (ms_step * 1e-3) / (BF16_PEAK_TFS * 1e12), 5),
+        "mfma_util": round(flops / (ms_step * 1e-3) /
+                           ((FP4_PEAK_TFS if dtype == "mxfp4" else BF16_PEAK_TFS) * 1e12), 5),
         "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": None,

@@ -1,0 +1,271 @@
+// kern_fp4.hip -- native MXFP4 expert GEMMs on the gfx950 scaled matrix cores
+// (v_mfma_scale_f32_16x16x128_f8f6f4, both operands e2m1 with one ue8m0 scale per 32).
+//
+// The weights feed the matrix cores exactly as stored (no decode); the activations are
+// the reference's MXFP4 quantization of the GEMM inputs (fp4_activation_qdq, block 32),
+// made by k_quantize_mxfp4.  Every product of two e2m1 values times two powers of two
+// is exact, so the result differs from the composed reference (QDQ, then the f32
+// moe_block maths) only by summation order.
+//
+// Operand layout of the 16x16x128 step (lane l, t = l % 16, q = l / 16): A row t and B
+// column t hold K elements [32 q, 32 q + 32) -- 16 bytes of packed codes, low nibble
+// first -- and the lane's scale operand is the ue8m0 byte of that 32-block; the result
+// is C[4 q + i][t], i = 0..3, as for the bf16 16x16 MFMAs.
+//
+// Tiling as the bf16 grouped GEMM (row tiles MT = 1, 2 or 4: the 128-row class spills):
+// a workgroup of 8 waves serves (item, column block),
+// each wave two 16-column tiles (gate and up at the same columns for the dual
+// projection, two adjacent tiles of the down matrix otherwise) over MT row tiles; K
+// advances 256 per step; the item's activation codes and scales of a step are staged in
+// LDS (double buffered, registers loaded two steps ahead), the weights of a step are
+// loaded two steps ahead into registers: per tile and lane two 16-byte loads (row t,
+// bytes 64 s + 16 q) and one 8-byte scale load (row t, the step's 8 blocks).
+#include "mfma_common.h"
+
+namespace mvllm_hip {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+struct F4Item {
+    int a, r0, nrow, pad;
+};
+
+struct F4Args {
+    const ExpertWork *ew;
+    const F4Item *items;
+    const uint8_t *acode;   // [rcap][K/2]
+    const uint8_t *ascale;  // [rcap][K/32]
+    float *hout;            // dual: H f32 [rcap][O]
+    float *out;             // single: Y f32 [rcap][O]
+    int nbn, K, O, rcap;
+    int act;
+    float act_a, act_b;
+};
+
+constexpr int kF4Threads = 512;
+constexpr int kF4Pitch = 128 + 16;  // LDS bytes per A row of codes (+16: banks)
+
+__host__ __device__ constexpr int f4_stage_bytes(int mt) {
+    return 16 * mt * kF4Pitch + 16 * mt * 8;
+}
+
+size_t fp4_lds_bytes(int mt) { return 2 * (size_t)f4_stage_bytes(mt); }
+
+struct F4Step {
+    u32x4 w[2][2];  // tile m, MFMA step s: row t, bytes 64 s + 16 q of the 128-byte step
+    u32x2 s[2];     // tile m: row t's 8 scale bytes of the step
+};
+
+template <bool DUAL, int MT>
+__global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
+    constexpr int BM = 16 * MT;
+    constexpr int STAGE = f4_stage_bytes(MT);
+    constexpr int CCH = (BM * 8 + kF4Threads - 1) / kF4Threads;  // 16-byte code chunks/thread
+    constexpr int PA = MT >= 8 ? 1 : 2;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+
+    const int item = blockIdx.x / A.nbn;
+    const int nb = blockIdx.x - item * A.nbn;
+    const F4Item it = A.items[item];
+    const ExpertWork &ew = A.ew[it.a];
+    const int K = A.K, O = A.O, nrow = it.nrow;
+    const int jbase = ew.row0 + it.r0;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63, t = lane & 15, q = lane >> 4;
+    const int col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
+    const uint32_t rowb = (uint32_t)(K >> 1), srow = (uint32_t)(K >> 5);
+
+    __amdgpu_buffer_rsrc_t rw[2], rs[2];
+    uint32_t vw[2], vs[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const int mi = DUAL ? m : 2;
+        const int trow = DUAL ? col0 : col0 + 16 * m;
+        rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
+        rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
+        vw[m] = (uint32_t)(trow + t) * rowb + 16u * (uint32_t)q;
+        vs[m] = (uint32_t)(trow + t) * srow;
+    }
+    auto load_b = [&] __attribute__((always_inline)) (F4Step &b, int k) {
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                b.w[m][s] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[m], vw[m] + 64 * s,
+                                                                 (uint32_t)k * 128u, 0));
+            b.s[m] = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[m], vs[m], (uint32_t)k * 8u, 0));
+        }
+    };
+
+    // A staging: code chunk c -> row c / 8, 16-byte column c % 8; scales: thread r < BM
+    // takes row r's 8 bytes.  Rows past nrow re-read the last row (never stored).
+    struct AStage {
+        u32x4 v[CCH];
+        u32x2 sc;
+    };
+    auto load_a = [&] __attribute__((always_inline)) (AStage &ra, int k) {
+#pragma unroll
+        for (int u = 0; u < CCH; ++u) {
+            const int c = u * kF4Threads + tid;
+            const int r = min((c >> 3) % BM, nrow - 1), cc = c & 7;
+            ra.v[u] = *reinterpret_cast<const u32x4 *>(A.acode + (size_t)(jbase + r) * rowb +
+                                                       (size_t)k * 128 + 16 * cc);
+        }
+        const int r = min(tid % BM, nrow - 1);
+        ra.sc = *reinterpret_cast<const u32x2 *>(A.ascale + (size_t)(jbase + r) * srow +
+                                                 (size_t)k * 8);
+    };
+    auto store_a = [&] __attribute__((always_inline)) (const AStage &ra, int buf) {
+        char *base = smem + buf * STAGE;
+#pragma unroll
+        for (int u = 0; u < CCH; ++u) {
+            const int c = u * kF4Threads + tid;
+            if (c < BM * 8)
+                *reinterpret_cast<u32x4 *>(base + (c >> 3) * kF4Pitch + 16 * (c & 7)) = ra.v[u];
+        }
+        if (tid < BM)
+            *reinterpret_cast<u32x2 *>(base + BM * kF4Pitch + 8 * tid) = ra.sc;
+    };
+
+    f4v acc[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+        acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&] __attribute__((always_inline)) (const F4Step &b, int buf) {
+        const char *base = smem + buf * STAGE;
+        const uint8_t *lsc = reinterpret_cast<const uint8_t *>(base + BM * kF4Pitch);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            i32x8 bv[2];
+            int sb[2];
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                const u32x4 w = b.w[m][s];
+                bv[m] = i32x8{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const int blk = 4 * s + q;  // this lane's 32-block among the step's 8
+                const uint32_t word = blk < 4 ? b.s[m].x : b.s[m].y;
+                sb[m] = (int)((word >> (8 * (blk & 3))) & 0xffu);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int row = mt * 16 + t;
+                const u32x4 av = *reinterpret_cast<const u32x4 *>(base + row * kF4Pitch + 64 * s +
+                                                                  16 * q);
+                const i32x8 a8 = i32x8{(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
+                const int sa = (int)lsc[row * 8 + 4 * s + q];
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    acc[mt][m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        a8, bv[m], acc[mt][m], 4, 4, 0, sa, 0, sb[m]);
+            }
+        }
+    };
+
+    // pipeline as the bf16 grouped GEMM (weights two steps ahead, activations staged one
+    // step ahead from registers loaded PA steps ahead; no branches around the loads)
+    const int nk = K / 256;
+    F4Step b0, b1;
+    AStage ra0, ra1;
+    load_a(ra0, 0);
+    if constexpr (PA == 2)
+        load_a(ra1, min(1, nk - 1));
+    load_b(b0, 0);
+    load_b(b1, 1);
+    store_a(ra0, 0);
+    __syncthreads();
+    for (int k = 0; k < nk; k += 2) {
+        if constexpr (PA == 2)
+            load_a(ra0, min(k + 2, nk - 1));
+        else
+            load_a(ra1, min(k + 1, nk - 1));
+        compute(b0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b0, k + 2);
+        store_a(ra1, 1);
+        __syncthreads();
+        if (k + 1 >= nk)
+            break;
+        if constexpr (PA == 2)
+            load_a(ra1, min(k + 3, nk - 1));
+        else
+            load_a(ra0, min(k + 2, nk - 1));
+        compute(b1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b1, k + 3);
+        store_a(ra0, 0);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = mt * 16 + 4 * q + i;
+            if (r >= nrow)
+                continue;
+            const size_t j = (size_t)(jbase + r);
+            if constexpr (DUAL) {
+                A.hout[j * O + col0 + t] =
+                    mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
+            } else {
+                A.out[j * O + col0 + t] = acc[mt][0][i];
+                A.out[j * O + col0 + 16 + t] = acc[mt][1][i];
+            }
+        }
+    }
+}
+
+template <bool DUAL, int MT>
+static hipError_t launch_f4_t(const F4Args &a, int n_items, hipStream_t st) {
+    const size_t lds = fp4_lds_bytes(MT);
+    auto kern = k_gemm_fp4<DUAL, MT>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess)
+        return e;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(n_items * a.nbn)), dim3(kF4Threads), lds, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *items,
+                           int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,
+                           float *out, int K, int O, int rcap, int act, float act_a, float act_b,
+                           hipStream_t st) {
+    if (n_items <= 0)
+        return hipSuccess;
+    if (K % 256 || O % (dual ? 128 : 256))
+        return hipErrorInvalidValue;
+    F4Args a{};
+    a.ew = ew;
+    a.items = static_cast<const F4Item *>(items);
+    a.acode = acode;
+    a.ascale = ascale;
+    a.hout = hout;
+    a.out = out;
+    a.nbn = O / (dual ? 128 : 256);
+    a.K = K;
+    a.O = O;
+    a.rcap = rcap;
+    a.act = act;
+    a.act_a = act_a;
+    a.act_b = act_b;
+#define MVLLM_F4(D_)                                                                          \
+    switch (mt) {                                                                             \
+    case 1: return launch_f4_t<D_, 1>(a, n_items, st);                                        \
+    case 2: return launch_f4_t<D_, 2>(a, n_items, st);                                        \
+    case 4: return launch_f4_t<D_, 4>(a, n_items, st);                                        \
+    default: return hipErrorInvalidValue;                                                     \
+    }
+    if (dual) {
+        MVLLM_F4(true)
+    }
+    MVLLM_F4(false)
+#undef MVLLM_F4
+}
+
+}  // namespace mvllm_hip

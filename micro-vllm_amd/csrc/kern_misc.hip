@@ -61,26 +61,17 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t st) {
 
 // ---- MXFP4 activation quantization (src/quant/native_act.cpp:159-179, block 32) ----
 
-// e2m1 magnitudes in code order 0..7
-__device__ __forceinline__ float e2m1_mag(int c) {
-    const int e = (c >> 1) & 3, m = c & 1;
-    return e == 0 ? 0.5f * (float)m : (1.f + 0.5f * (float)m) * (float)(1 << (e - 1));
-}
-
-// Nearest code with the reference's scan order 0..15 and strict '<' (lowest index wins
-// ties).  Codes 8..15 are the negatives and code 8 decodes to +0 there.
-__device__ __forceinline__ int nearest_e2m1(float v) {
-    int best = 0;
-    float dist = fabsf(v);
-    for (int c = 1; c < 16; ++c) {
-        const float val = c == 8 ? 0.f : (c & 8 ? -e2m1_mag(c & 7) : e2m1_mag(c));
-        const float d = fabsf(v - val);
-        if (d < dist) {
-            dist = d;
-            best = c;
-        }
-    }
-    return best;
+// Nearest e2m1 code to q in [-6, 6] with the reference's rule (scan of codes 0..15 with
+// strict '<': the lowest index wins a tie).  The positive magnitudes are codes 0..7
+// {0, .5, 1, 1.5, 2, 3, 4, 6}; a tie between two of them goes to the smaller one, and a
+// result of zero is always code 0 (code 8, -0, comes later in the scan).  So: round |q|
+// to the grid with ties toward zero, then set the sign bit for negative non-zero codes.
+// NaN never gets here: clamping with fminf/fmaxf maps it to 6 first, as in the reference.
+__device__ __forceinline__ int nearest_e2m1(float q) {
+    const float m = fabsf(q);
+    const int c = (m > 0.25f) + (m > 0.75f) + (m > 1.25f) + (m > 1.75f) + (m > 2.5f) +
+                  (m > 3.5f) + (m > 5.f);
+    return (q < 0.f && c > 0) ? (c | 8) : c;
 }
 
 // ceil(log2(v)) for v >= 2^-126 (frexp exponent, minus one at exact powers of two).
@@ -94,40 +85,83 @@ __device__ __forceinline__ int ceil_log2_normal(float v) {
     return (b & 0x7fffffu) == 0 ? ef - 127 : ef - 126;
 }
 
-// one thread per 32-element block
-__global__ void k_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales) {
-    const int nb = K / 32;
-    const size_t total = (size_t)n * nb;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < total;
-         i += (size_t)gridDim.x * blockDim.x) {
-        const size_t row = i / nb, blk = i % nb;
-        const float *xb = x + row * (size_t)K + blk * 32;
-        float amax = 0.f;
-        for (int k = 0; k < 32; ++k) {
-            const float a = fabsf(xb[k]);
-            if (a > amax)
-                amax = a;
+// Eight lanes per 32-element block, four elements per lane (one 16-byte load), eight
+// blocks per wave and QU blocks per lane in flight.  The block maximum is reduced
+// across the 8 lanes; each lane packs its 4 codes into 2 bytes (low nibble = even
+// element).  Output row j reads input row rows_map[j] (or j).  Indices are 32-bit: the
+// launcher refuses more than 2^31 blocks.
+constexpr int kQU = 4;
+
+__global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const int *rows_map,
+                                                        int n, int K, uint8_t *codes,
+                                                        uint8_t *scales) {
+    const uint32_t nb = (uint32_t)(K / 32);
+    const uint32_t total = (uint32_t)n * nb;  // blocks
+    const uint32_t lane = threadIdx.x & 63, e8 = lane & 7;
+    const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const uint32_t nwaves = (gridDim.x * blockDim.x) >> 6;
+    // wave-uniform loop bound: every shuffle below sees the whole wave
+    for (uint32_t b0 = wave * 8 * kQU; b0 < total; b0 += nwaves * 8 * kQU) {
+        float4 v[kQU];
+        uint32_t row[kQU], blk[kQU];
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) {
+            const uint32_t bid = b0 + 8 * u + (lane >> 3);
+            const bool ok = bid < total;
+            row[u] = ok ? bid / nb : 0;
+            blk[u] = ok ? bid - row[u] * nb : 0;
+            const uint32_t src = rows_map ? (uint32_t)rows_map[row[u]] : row[u];
+            v[u] = ok ? *reinterpret_cast<const float4 *>(x + (size_t)src * K + blk[u] * 32 +
+                                                          4 * e8)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        amax = fmaxf(amax, 6.f * 1.1754943508222875e-38f);  // 6 * 2^-126
-        int ex = ceil_log2_normal(amax / 6.f);
-        ex = ex < -127 ? -127 : (ex > 127 ? 127 : ex);
-        const uint32_t sc = (uint32_t)(ex + 127);
-        scales[i] = (uint8_t)sc;
-        const float scale = ldexpf(1.f, ex);
-        uint8_t *cb = codes + row * (size_t)(K / 2) + blk * 16;
-        for (int k = 0; k < 32; k += 2) {
-            const float q0 = fmaxf(-6.f, fminf(6.f, xb[k] / scale));
-            const float q1 = fmaxf(-6.f, fminf(6.f, xb[k + 1] / scale));
-            cb[k >> 1] = (uint8_t)(nearest_e2m1(q0) | (nearest_e2m1(q1) << 4));
+#pragma unroll
+        for (int u = 0; u < kQU; ++u) {
+            const uint32_t bid = b0 + 8 * u + (lane >> 3);
+            const float f[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            float amax = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float a = fabsf(f[i]);
+                if (a > amax)  // NaN never wins (the reference's '>' test)
+                    amax = a;
+            }
+#pragma unroll
+            for (int o = 4; o >= 1; o >>= 1)
+                amax = fmaxf(amax, __shfl_xor(amax, o, 8));
+            amax = fmaxf(amax, 6.f * 1.1754943508222875e-38f);  // 6 * 2^-126
+            int ex = ceil_log2_normal(amax / 6.f);
+            ex = ex < -127 ? -127 : (ex > 127 ? 127 : ex);
+            // x / 2^ex == x * 2^-ex exactly (both round the same real number); 2^-127 is
+            // subnormal, so that one case divides
+            const float inv = __uint_as_float((uint32_t)(127 - ex) << 23);
+            uint32_t packed = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float sc = ex == 127 ? f[i] / ldexpf(1.f, 127) : f[i] * inv;
+                const float q = fmaxf(-6.f, fminf(6.f, sc));
+                packed |= (uint32_t)nearest_e2m1(q) << (4 * i);
+            }
+            if (bid < total) {
+                *reinterpret_cast<uint16_t *>(codes + (size_t)row[u] * (size_t)(K / 2) +
+                                              blk[u] * 16 + 2 * e8) = (uint16_t)packed;
+                if (e8 == 0)
+                    scales[bid] = (uint8_t)(ex + 127);
+            }
         }
     }
 }
 
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
-                                 hipStream_t st) {
-    if (n <= 0 || K <= 0 || K % 32)
+                                 hipStream_t st, const int *rows_map) {
+    if (n <= 0 || K <= 0 || K % 32 || (size_t)n * (K / 32) >= (size_t(1) << 31) ||
+        (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_quantize_mxfp4, dim3(1024), dim3(256), 0, st, x, n, K, codes, scales);
+    const size_t waves = ((size_t)n * (K / 32) + 8 * kQU - 1) / (8 * kQU);
+    const size_t wgs = (waves + 3) / 4;
+    const unsigned grid = (unsigned)(wgs < 4096 ? wgs : 4096);
+    hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid), dim3(256), 0, st, x, rows_map, n, K, codes,
+                       scales);
     return hipGetLastError();
 }
 

@@ -56,8 +56,9 @@ hipError_t launch_dequant_bf16path(int fmt, const void *packed, const void *scal
                                    int K, float *w, hipStream_t st);
 hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, int row16,
                            hipStream_t st);
+// MXFP4 activation quantization of n rows of K (row j = x row rows_map[j], or j).
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
-                                 hipStream_t st);
+                                 hipStream_t st, const int *rows_map = nullptr);
 
 // Matrix-core path (kern_mfma.hip).  The gate/up GEMM (dual) reads the f32 input rows
 // (compact row j = input row in_rows[j], or j) and splits them into `terms` bf16 terms
@@ -97,5 +98,18 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
                        float act_a, float act_b, hipStream_t st);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
                               int K, int rcap, void *planes, float *xs, hipStream_t st);
+
+// Native MXFP4 GEMM (kern_fp4.hip): v_mfma_scale_f32_16x16x128_f8f6f4 with e2m1 activations
+// (codes [rcap][K/2] + ue8m0 scales [rcap][K/32], from launch_quantize_mxfp4) against the
+// MXFP4 weights as stored.  Items and workgroup tiling as launch_gemm (mt 1, 2, 4);
+// the dual projection writes H = act(gate, up) as f32 [rcap][O], the single one Y.
+// Requires K % 256 == 0, O % 128 (dual) / % 256 (single) == 0, 16-byte aligned weights,
+// 8-byte aligned scales.
+constexpr int kFp4MaxMt = 4;
+size_t fp4_lds_bytes(int mt);
+hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *items,
+                           int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,
+                           float *out, int K, int O, int rcap, int act, float act_a, float act_b,
+                           hipStream_t st);
 
 }  // namespace mvllm_hip

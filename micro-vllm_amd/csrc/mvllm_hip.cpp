@@ -139,6 +139,7 @@ struct Ctx {
     int dequant_path = 0;    // mvllm_hip_dequant: 0 f32 decode, 1 matrix-core bf16 decode
     int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2 or 4
     int gemm = 0;            // grouped GEMM: 0 auto, 1 whenever it applies, 2 never
+    int fp4act = 0;          // MXFP4 experts: 1 = quantize activations, native FP4 GEMMs
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -265,6 +266,7 @@ struct GemmCls {
 struct CallCfg {
     bool mfma = false;        // decode-shaped matrix-core kernels
     bool gemm = false;        // grouped GEMM (prefill-shaped)
+    bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
@@ -347,7 +349,7 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
 // smallest class that holds it; classes ordered by mt, experts ascending within each.
 void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     cc.terms = cc.terms >= 2 ? 2 : 1;
-    const int max_mt = gemm_max_mt(fmt, cc.terms);
+    const int max_mt = cc.fp4 ? kFp4MaxMt : gemm_max_mt(fmt, cc.terms);
     const int bm = 16 * max_mt;
     std::vector<int> per[4];  // class index = log2(mt)
     size_t split_at[4] = {0, 0, 0, 0};
@@ -392,13 +394,20 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
               I <= kDecMaxK && aligned(in, 16);
     // (% 1024 also covers the O % 512 == 0 that 16-wave workgroups of 2-tile waves need)
     bool gok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && aligned(in, 16);
+    const size_t walign = fmt == 7 && C.fp4act ? 16 : 8;  // the FP4 GEMM loads 16-byte rows
     int most = 0;
     for (const ExpertWork &w : P.ew) {
         most = std::max(most, w.nrows);
         for (int m = 0; m < 3; ++m) {
             ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], 4);
-            gok = gok && aligned(w.w[m], 8) && aligned(w.s[m], fmt == 4 ? 16 : 8);
+            gok = gok && aligned(w.w[m], walign) && aligned(w.s[m], fmt == 4 ? 16 : 8);
         }
+    }
+    // native MXFP4 activations (opt-in): the scaled FP4 GEMM for every row count
+    if (fmt == 7 && C.fp4act && gok) {
+        cc.fp4 = true;
+        plan_gemm(cc, P, split, fmt);
+        return;
     }
     // grouped GEMM when forced, or when some expert has more rows than one decode item
     if (gok && C.gemm != 2 && (C.gemm == 1 || most > 16)) {
@@ -519,7 +528,40 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             HIP_TRY(hipEventCreate(&e));
         HIP_TRY(hipEventRecord(tc.ev[0], st));
     }
-    if (cc.gemm) {
+    if (cc.fp4) {
+        // activations quantized to MXFP4 (bit-exact with fp4_activation_qdq), the gate/up
+        // GEMM writes H f32, H is quantized, the down GEMM writes Y
+        HIP_TRY(C.Xp.ensure(std::max<size_t>(R * (D / 2 + D / 32), 256)));
+        HIP_TRY(C.Ph.ensure(std::max<size_t>(R * (I / 2 + I / 32), 256)));
+        uint8_t *xq = static_cast<uint8_t *>(C.Xp.p), *xsc = xq + R * (D / 2);
+        uint8_t *hq = static_cast<uint8_t *>(C.Ph.p), *hsc = hq + R * (I / 2);
+        float *H = static_cast<float *>(C.H.p);
+        HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows));
+        for (int part = 0; part < 2; ++part) {
+            if (part == 1 && gate_event)
+                HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+            for (int c = 0; c < cc.n_gcls; ++c) {
+                const GemmCls &g = cc.gcls[c];
+                const size_t i0 = part ? g.it_split : g.it0, i1 = part ? g.it1 : g.it_split;
+                if (i1 <= i0)
+                    continue;
+                HIP_TRY(launch_gemm_fp4(true, g.mt, dp.ew, dp.items + 4 * i0,
+                                        static_cast<int>(i1 - i0), xq, xsc, H, nullptr, D, I,
+                                        rcap, act, a, b, st));
+                C.stats[13] += 1;
+            }
+        }
+        HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st));
+        if (C.timing)
+            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        for (int c = 0; c < cc.n_gcls; ++c) {
+            const GemmCls &g = cc.gcls[c];
+            HIP_TRY(launch_gemm_fp4(false, g.mt, dp.ew, dp.items + 4 * g.it0,
+                                    static_cast<int>(g.it1 - g.it0), hq, hsc, nullptr,
+                                    static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
+            C.stats[14] += 1;
+        }
+    } else if (cc.gemm) {
         const size_t tb = (size_t)cc.terms * 2;
         HIP_TRY(C.Xp.ensure(std::max<size_t>(tb * R * D, 256)));
         HIP_TRY(C.XS.ensure(std::max<size_t>((size_t)(D / 64) * 4 * R * 4, 256)));
@@ -770,6 +812,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return 0;
         C.dec_ks = static_cast<int>(value);
+    } else if (k == "fp4act") {
+        C.fp4act = value ? 1 : 0;
     } else if (k == "gemm") {
         if (value < 0 || value > 2)
             return 0;

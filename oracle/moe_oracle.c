@@ -432,3 +432,68 @@ int orc_fp4_activation_qdq(float *output, uint8_t *scales, const float *input, i
     }
     return 0;
 }
+
+
+/* ---- native-FP4 composition (the checker of the MXFP4-activation path) -------
+ * The reference moe_block (src/gpu/metal_ops.cpp:278-342) with the input of each GEMM
+ * passed through the reference's MXFP4 activation quantize-dequantize
+ * (fp4_activation_qdq, block 32, src/quant/native_act.cpp:159-179) row by row: x rows
+ * before gate/up, h rows before down.  fmt must be 7; validation and skip rules are
+ * moe_block's. */
+static void qdq_rows(float *dst, const float *src, int n, int len, uint8_t *sc) {
+    for (int r = 0; r < n; ++r)
+        orc_fp4_activation_qdq(dst + (size_t)r * len, sc, src + (size_t)r * len, len, 32, NULL);
+}
+
+int orc_moe_block_fp4act(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                         const void *const *u, const void *const *d, const float *const *gs,
+                         const float *const *us, const float *const *ds, const float *xg,
+                         const int *xoff, const int *nr, const int *rows, const float *rw,
+                         float *out, int S, int act, float act_a, float act_b) {
+    (void)qgs;
+    if (nb < 1 || D < 1 || !out || !xg || fmt != 7 || !xoff || !nr)
+        return 0;
+    int base = 0;
+    for (int e = 0; e < nb; ++e) {
+        const int nre = nr[e];
+        if (nre <= 0)
+            continue;
+        if (Iinter < 1 || !g || !u || !d || !g[e] || !u[e] || !d[e] || !gs || !us || !ds ||
+            !gs[e] || !us[e] || !ds[e]) {
+            base += nre;
+            continue;
+        }
+        const size_t ni = (size_t)nre * (size_t)Iinter, nd = (size_t)nre * (size_t)D;
+        float *xq = (float *)calloc(nd, sizeof(float));
+        float *gate = (float *)calloc(ni, sizeof(float));
+        float *up = (float *)calloc(ni, sizeof(float));
+        float *hq = (float *)calloc(ni, sizeof(float));
+        float *hh = (float *)calloc(nd, sizeof(float));
+        uint8_t *sc = (uint8_t *)calloc((size_t)(D > Iinter ? D : Iinter) / 32 + 1, 1);
+        if (!xq || !gate || !up || !hq || !hh || !sc) {
+            free(xq); free(gate); free(up); free(hq); free(hh); free(sc);
+            return 0;
+        }
+        qdq_rows(xq, xg + (size_t)xoff[e] * (size_t)D, nre, D, sc);
+        orc_matmul_mxfp4(gate, xq, (const uint8_t *)g[e], (const uint8_t *)gs[e], nre, D, Iinter);
+        orc_matmul_mxfp4(up, xq, (const uint8_t *)u[e], (const uint8_t *)us[e], nre, D, Iinter);
+        orc_apply_act(gate, up, nre * Iinter, act, act_a, act_b);
+        qdq_rows(hq, gate, nre, Iinter, sc);
+        orc_matmul_mxfp4(hh, hq, (const uint8_t *)d[e], (const uint8_t *)ds[e], nre, Iinter, D);
+        if (rows && rw) {
+            for (int r = 0; r < nre; ++r) {
+                const int dest = rows[base + r];
+                if (dest < 0 || (S > 0 && dest >= S))
+                    continue;
+                const float wgt = rw[base + r];
+                float *orow = out + (size_t)dest * (size_t)D;
+                const float *hrow = hh + (size_t)r * (size_t)D;
+                for (int i = 0; i < D; ++i)
+                    orow[i] += wgt * hrow[i];
+            }
+        }
+        free(xq); free(gate); free(up); free(hq); free(hh); free(sc);
+        base += nre;
+    }
+    return 1;
+}

@@ -76,6 +76,16 @@ int orc_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int *
                      int *nr, int *rows, float *rw, int cap_experts, int cap_rows,
                      int *n_rows_out);
 
+/* moe_block with MXFP4-quantized GEMM inputs: fp4_activation_qdq (block 32) on the x rows
+ * before gate/up and on the h rows before down, fmt 7 only -- the checker of the native
+ * scaled-FP4 matrix-core path (src/gpu/metal_ops.cpp:278-342 composed with
+ * src/quant/native_act.cpp:159-179). */
+int orc_moe_block_fp4act(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
+                         const void *const *u, const void *const *d, const float *const *gs,
+                         const float *const *us, const float *const *ds, const float *xg,
+                         const int *xoff, const int *nr, const int *rows, const float *rw,
+                         float *out, int S, int act, float act_a, float act_b);
+
 /* Native activation codecs: src/quant/native_act.cpp:24-88, 159-179.
  * codes (nullable) receives the chosen e2m1 code per element. */
 float orc_e8m0_decode(uint8_t v);

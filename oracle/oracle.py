@@ -82,6 +82,8 @@ class CpuMoe:
                 "dequant_mxfp4": (None, [_p, _p, _p, _i, _i]),
                 "moe_segments": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
                 "fp4_activation_qdq": (_i, [_p, _p, _p, _i, _i, _p]),
+                "moe_block_fp4act": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p,
+                                          _p, _p, _p, _p, _p, _i, _i, _f, _f]),
             }.items():
                 fn = getattr(L, f"orc_{name}")
                 fn.restype, fn.argtypes = res, args
@@ -136,6 +138,15 @@ class CpuMoe:
         """
         pa = [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
         return self.fn("moe_block")(
+            nb, D, Iinter, fmt, qgs, *pa, _ptr(xg), _ptr(xoff), _ptr(nr), _ptr(rows), _ptr(rw),
+            _ptr(out), S, act, act_a, act_b)
+
+    def moe_block_fp4act(self, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw,
+                         out, S, act=0, act_a=0.0, act_b=0.0, qgs=0):
+        """moe_block with MXFP4-quantized GEMM inputs (the native-FP4 path's checker;
+        restatement only)."""
+        pa = [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
+        return self.lib.orc_moe_block_fp4act(
             nb, D, Iinter, fmt, qgs, *pa, _ptr(xg), _ptr(xoff), _ptr(nr), _ptr(rows), _ptr(rw),
             _ptr(out), S, act, act_a, act_b)
 

@@ -347,3 +347,64 @@ def test_ref_topk_union_qdq_bit_exact(orc, ref):
         assert a[0] == b[0] == 0
         assert np.array_equal(a[2], b[2])
         assert np.array_equal(_bits(a[1]), _bits(b[1]))
+
+
+# ---------------------------------------------------------------- native-FP4 composition
+
+def _compose_fp4act_ref(lib, c, act, a, b):
+    """The same composition built in Python from the reference build's own pieces
+    (fp4_activation_qdq, matmul_mxfp4, the activation scalars) -- a second route to the
+    numbers orc_moe_block_fp4act must produce bit for bit."""
+    out = c.out.copy()
+    actf = {0: lambda g, u: np.float32(lib.fn("sigmoid")(g)) * np.float32(g) * np.float32(u),
+            1: lambda g, u: lib.fn("clamped_swiglu")(g, u, a),
+            2: lambda g, u: lib.fn("situ_glu")(g, u, a, b)}[act]
+    base = 0
+    for e in range(c.nb):
+        n = int(c.nr[e])
+        if n <= 0:
+            continue
+        if c.g[e] is None:
+            base += n
+            continue
+        xe = c.xg[int(c.xoff[e]):int(c.xoff[e]) + n]
+        xq = np.stack([lib.fp4_activation_qdq(r, 32)[1] for r in xe])
+        gt = lib.matmul(7, xq, c.g[e], c.gs[e])
+        up = lib.matmul(7, xq, c.u[e], c.us[e])
+        h = np.array([[actf(float(gv), float(uv)) for gv, uv in zip(gr, ur)]
+                      for gr, ur in zip(gt, up)], np.float32)
+        hq = np.stack([lib.fp4_activation_qdq(r, 32)[1] for r in h])
+        y = lib.matmul(7, hq, c.d[e], c.ds[e])
+        for r in range(n):
+            dst = int(c.rows[base + r])
+            if 0 <= dst < c.S:
+                out[dst] = out[dst] + np.float32(c.rw[base + r]) * y[r]
+        base += n
+    return out
+
+
+@pytest.mark.parametrize("act,a,b", [(2, 4.0, 25.0), (1, 7.0, 0.0)])
+def test_fp4act_composition(orc, ref, act, a, b):
+    """orc_moe_block_fp4act equals the composition of the reference build's own QDQ,
+    MXFP4 GEMM and activation, bit for bit (silu_mul's product order is pinned by the
+    moe_block tests; here the clamped and SiTU activations are composed)."""
+    rng = np.random.default_rng(71 + act)
+    c = random_case(rng, 7, 64, 96, [2, 0, 3, 1], 4, act, a, b, null_experts=(3,), invalid_rows=1)
+    o1 = c.out.copy()
+    assert orc.moe_block_fp4act(*c.args(o1), act, a, b) == 1
+    o2 = _compose_fp4act_ref(ref, c, act, a, b)
+    assert np.array_equal(o1.view(np.uint32), o2.view(np.uint32))
+
+
+def test_fp4act_close_to_f32(orc):
+    """Quantizing activations to MXFP4 moves the block output by a bounded amount (the
+    e2m1 grid is 1 part in 8 at worst), and fmt != 7 is refused."""
+    rng = np.random.default_rng(72)
+    c = random_case(rng, 7, 256, 128, [3, 2], 3, 2, 4.0, 25.0, zero_out=True)
+    o1, o2 = c.out.copy(), c.out.copy()
+    assert orc.moe_block_fp4act(*c.args(o1), 2, 4.0, 25.0) == 1
+    assert orc.moe_block(*c.args(o2), 2, 4.0, 25.0) == 1
+    err = npref.rel_err(o1, o2)
+    assert 1e-4 < err < 0.3
+    c4 = random_case(rng, 4, 64, 64, [1], 1)
+    assert orc.moe_block_fp4act(*c4.args(), 0, 0.0, 0.0) == 0
