@@ -24,6 +24,21 @@ FP4_PEAK_TFS = 10100.0
 BF16_PEAK_TFS = 2500.0
 
 
+def traffic_bytes(workload, phase):
+    """HBM bytes per launch of the workload's gate/up kernel as measured with rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json, calibrated against a copy of
+    known size), or None when that workload has not been measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    for k, v in d.get(workload, {}).items():
+        if k.endswith(phase):
+            return v.get("bytes")
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -59,11 +74,17 @@ def main():
     ap.add_argument("--config", default="c1")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--mode", type=int, default=0)
+    ap.add_argument("--opt", action="append", default=[], metavar="KEY=VALUE",
+                    help="extra mvllm_hip_set_option settings (e.g. dec_ks=2)")
     ap.add_argument("--fp4act", action="store_true",
                     help="MXFP4 experts: quantize activations, native scaled-FP4 matrix cores")
     ap.add_argument("--pool-gb", type=float, default=4.5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--staged", type=float, default=None, metavar="MISS_RATE",
+                    help="drop-in host entry with the HBM expert tier: this fraction of each "
+                         "step's experts is not resident and is copied from pinned host "
+                         "memory by the call (config c2 uses 0.25)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -83,6 +104,13 @@ def main():
     mvllm_hip.init(0)
     mvllm_hip.set_option("mode", args.mode)
     mvllm_hip.set_option("fp4act", 1 if args.fp4act else 0)
+    for kv in args.opt:
+        k, v = kv.split("=", 1)
+        if not mvllm_hip.set_option(k, int(v)):
+            raise SystemExit(f"option {kv} refused")
+
+    if args.staged is not None:
+        return staged(args, np, torch, mvllm_hip, synth, cfg, T)
 
     w = synth.make_workload(args.config, T=T, with_experts=False)
     nbytes, _ = mvllm_hip.expert_geom(fmt, D, I)
@@ -169,7 +197,14 @@ def main():
     sink = torch.zeros(4096, dtype=torch.uint8, device="cuda")
     probe_bytes = (pool.numel() // 4096) * 4096
     hbm_gbs = probe_bytes / mvllm_hip.membench(0, pool, sink, probe_bytes, 0, 5) / 1e6
-    log(f"HBM stream-read probe: {hbm_gbs:.0f} GB/s over {probe_bytes / 2**30:.2f} GiB")
+    # copy probe (1 GiB read + 1 GiB written): with the read probe, the known byte counts
+    # that calibrate the FETCH_SIZE / WRITE_SIZE counters of a profiled run
+    copy_bytes = min(1 << 30, probe_bytes)
+    dst = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
+    copy_gbs = 2 * copy_bytes / mvllm_hip.membench(1, pool, dst, copy_bytes, 0, 3) / 1e6
+    del dst
+    log(f"HBM stream-read probe: {hbm_gbs:.0f} GB/s over {probe_bytes / 2**30:.2f} GiB; "
+        f"copy probe {copy_gbs:.0f} GB/s (read + write) over {copy_bytes / 2**30:.2f} GiB")
 
     cpu = None
     if not args.no_cpu:
@@ -191,17 +226,108 @@ def main():
                 f"{n_blobs * nbytes / 2**30:.1f} GiB pool rotated per step)",
         "config": {"workload": f"{args.config} {cfg['desc']}, T={T}", "D": D, "I": I, "E": E,
                    "topk": k, "T": T, "fmt": fmt, "experts_per_step": int(w.nb),
-                   "rows": int(w.nr.sum()), "mode": args.mode, "fp4act": bool(args.fp4act)},
+                   "rows": int(w.nr.sum()), "mode": args.mode, "fp4act": bool(args.fp4act),
+                   "options": args.opt},
         "weight_gbps": round(wbytes / ms_step / 1e6, 1),
         "hbm_probe_gbps": round(hbm_gbs, 1),
+        "hbm_copy_probe_gbps": round(copy_gbs, 1),
         "mfma_util": round(flops / (ms_step * 1e-3) /
                            ((FP4_PEAK_TFS if dtype == "mxfp4" else BF16_PEAK_TFS) * 1e12), 5),
         "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": traffic_bytes(f"{args.config} T={T}", "gate_up"),
                      "bytes_per_launch": int(w.nb * b_gu), "avg_launch_us": round(ms_gu * 1e3, 3)},
         "phases_us": {"gate_up": round(ms_gu * 1e3, 3), "down": round(ms_dn * 1e3, 3),
                       "combine": round(ms_cb * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+def staged(args, np, torch, mvllm_hip, synth, cfg, T):
+    """One step = one drop-in mvllm_hip_moe_block call on host pointers (activations and
+    output in host memory, as the engine calls it).  Expert blobs live in one pinned host
+    buffer (the ExpertStore slots); most are promoted into the library's HBM tier at set-up,
+    the rest are host-only, and each step draws round(miss_rate * nb) of its experts from
+    them, so the call copies those blobs in on its copy stream while the resident experts
+    compute.  Resident and host-only sets rotate over more than the Infinity Cache holds."""
+    import ctypes
+    D, I, fmt = cfg["D"], cfg["I"], cfg["fmt"]
+    w = synth.make_workload(args.config, T=T, with_experts=False)
+    nbytes, off = mvllm_hip.expert_geom(fmt, D, I)
+    stride = (nbytes + 4095) // 4096 * 4096
+    n_miss = int(round(args.staged * w.nb))
+    n_res = w.nb - n_miss
+    r_res = max(n_res, int(np.ceil(1.2 * 2**30 / nbytes)))   # resident blobs (> 1 GiB)
+    r_host = max(n_miss, 2 * n_miss * 4)                      # host-only blobs
+    total = r_res + r_host
+    L = mvllm_hip.lib()
+    host = L.mvllm_hip_host_alloc(total * stride)
+    if not host:
+        raise SystemExit("pinned host allocation failed")
+    pool, pstride, poff, _ = build_pool(torch, mvllm_hip, fmt, D, I, total, 1234)
+    for b in range(total):  # reference layout, one slot per blob
+        src = pool[b, :nbytes].cpu().numpy()
+        ctypes.memmove(host + b * stride, src.ctypes.data, nbytes)
+    for b in range(r_res):
+        mvllm_hip.promote(host + b * stride, nbytes, 0, b)
+    torch.cuda.synchronize()
+    log(f"staged {args.config} T={T}: {w.nb} experts/step ({n_res} resident, {n_miss} misses), "
+        f"{r_res} resident + {r_host} host-only blobs of {nbytes / 2**20:.2f} MiB")
+    order = (0, 2, 4, 1, 3, 5)
+
+    def lists(s):
+        blobs = [(s * n_res + j) % r_res for j in range(n_res)] + \
+                [r_res + (s * n_miss + j) % r_host for j in range(n_miss)]
+        ptrs = [[], [], [], [], [], []]
+        for b in blobs:
+            for slot, oi in enumerate(order):
+                ptrs[slot].append(host + b * stride + int(off[oi]))
+        return ptrs
+
+    out = np.zeros((T, D), np.float32)
+
+    def step(s):
+        out[:] = 0.0
+        mvllm_hip.moe_block(w.nb, D, I, fmt, *lists(s), w.xg, w.xoff, w.nr, w.rows, w.rw, out,
+                            T, w.act, w.a, w.b)
+
+    for s in range(args.warmup):
+        step(s)
+    mvllm_hip.set_option("timing", 1)
+    mvllm_hip.stats_reset()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(args.warmup + s)
+    wall = (time.perf_counter() - t0) / args.steps
+    st = mvllm_hip.stats()
+    mvllm_hip.set_option("timing", 0)
+    ms_gu, ms_dn = st["ms_gate_up"] / args.steps, st["ms_down"] / args.steps
+    h2d = st["h2d_weight_bytes"] / args.steps
+    log(f"step {wall * 1e6:.1f} us: misses/step {st['misses'] / args.steps:.1f}, "
+        f"hits/step {st['resident_hits'] / args.steps:.1f}, staged {h2d / 2**20:.1f} MiB/step "
+        f"({h2d / wall / 1e9:.1f} GB/s over the step); gate/up {ms_gu * 1e3:.1f} us, "
+        f"down {ms_dn * 1e3:.1f} us (HIP events, compute stream)")
+    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+    b_gu = 2 * (I * (D // 2) + I * ((D + gq - 1) // gq) * sb)
+    gu_gbs = w.nb * b_gu / (ms_gu * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(np, torch, w, pool, pstride, poff, fmt, D, I, T, args.cpu_seconds)
+    rec = {
+        "metric": "moe_block tokens/s (decode), effective weight GB/s",
+        "value": round(T / wall, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 6), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16x2",
+        "data": "synthetic (seeded; weights random in the reference layouts, pinned host slots)",
+        "config": {"workload": f"{args.config} {cfg['desc']}, T={T}, drop-in host entry, "
+                               f"{n_miss} of {w.nb} experts staged from pinned host memory",
+                   "D": D, "I": I, "E": cfg["E"], "topk": cfg["k"], "T": T, "fmt": fmt,
+                   "miss_rate": args.staged, "includes": "PCIe H2D of misses, xg and out"},
+        "staged_mib_per_step": round(h2d / 2**20, 2),
+        "roofline": {"bound": "hbm", "kernel": "gate_up (resident + staged experts)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
