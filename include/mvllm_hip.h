@@ -75,17 +75,30 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
                             int act, float act_a, float act_b, void *stream);
 
 /* Options (key, value); returns 1 if the key and value are accepted.
- *   "mode"   how activations enter the matrix cores (weights are always decoded
+ *   "mode"   how activations enter the bf16 matrix cores (weights are always decoded
  *            exactly; products and sums are f32):
- *            0  default: each f32 activation as 2 bf16 terms (hi + lo; represents the
- *               value to 2^-17 relative, below the reference's own f32 summation noise)
- *            1  3 bf16 terms (the activation exactly)
- *            2  1 bf16 term (bf16 activations; ~2^-9 relative)
+ *            0  default: decode-shaped calls split each f32 activation into 2 bf16 terms
+ *               (hi + lo; 2^-17 relative); the prefill grouped GEMM uses 1 term (bf16)
+ *            1  3 terms in the decode kernels (the activation exactly), 2 in the GEMM
+ *            2  1 bf16 term everywhere
+ *   "gemm"   0 = automatic (the grouped GEMM when some expert has more than 16 rows, or
+ *            the decode kernels do not fit the shape), 1 = grouped GEMM whenever it
+ *            applies, 2 = never.
+ *   "fp4act" 1 = MXFP4 experts (fmt 7) run on native MXFP4 activations: the GEMM inputs
+ *            (x, then h) are quantized exactly as fp4_activation_qdq with block 32
+ *            (src/quant/native_act.cpp:159-179) and fed with the weights as stored to the
+ *            scaled FP4 matrix cores.  Changes the numbers (activation quantization);
+ *            weight scale bytes 0 and 255 act as the hardware's 2^-127 and NaN, not the
+ *            reference's +0 and +inf.
+ *   "combine_ordered" 1 = decode calls also run the separate combine kernel, which
+ *            applies out[t] += w * y in the reference's expert order (bit-exact given the
+ *            same expert outputs); by default decode folds the combine into the down
+ *            kernel with float atomics (same products, any summation order).
  *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
  *   "dec_ks" 0 = automatic; 1, 2 or 4 forces the split of K across waves.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
  * Shapes the matrix-core kernels do not take (fmt 0, D or Iinter not a multiple of
- * 1024 or above 8192, misaligned pointers) run an exact f32 kernel instead. */
+ * 256, misaligned pointers) run an exact f32 kernel instead. */
 int mvllm_hip_set_option(const char *key, long long value);
 
 /* ---- segment construction: moe_union_ids (src/model/ops.cpp:1082-1099) and the

@@ -68,7 +68,9 @@ struct DecArgs {
     const float *xs;      // single, fmt 4: H partial sums [K/64][4][rcap]
     __bf16 *pout;         // dual: H planes [TERMS][rcap][O]
     float *hp;            // dual, fmt 4: H partial sums [O/64][4][rcap]
-    float *out;           // single: Y [rcap][O] f32
+    float *out;           // single: Y [rcap][O] f32, or the caller's out [S][O] when dest
+    const int *dest;      // single, optional: compact row -> row of out; the epilogue then
+    const float *wrow;    // adds wrow[j] * y into out (float atomics) instead of writing Y
     int wgs;              // workgroups per item = O / (16 * TW * TPW)
     int K, O, rcap, rmax;
     int act;
@@ -476,8 +478,13 @@ __global__ __launch_bounds__(kDecThreads) void k_mfma_dec(DecArgs A) {
                         A.hp[((size_t)(tile >> 2) * 4 + (tile & 3)) * A.rcap + j] = rep;
                 }
             } else {
-                if (tok < nrow)
-                    A.out[(size_t)j * O + o] = fin[r][0][i];
+                if (tok < nrow) {
+                    if (A.dest)  // top-k combine folded in: out[dest] += w * y
+                        unsafeAtomicAdd(A.out + (size_t)A.dest[j] * O + o,
+                                        __fmul_rn(A.wrow[j], fin[r][0][i]));
+                    else
+                        A.out[(size_t)j * O + o] = fin[r][0][i];
+                }
             }
         }
     }
@@ -531,7 +538,7 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const
                            const void *items, int n_items, const float *xin, const int *in_rows,
                            const void *pin, const float *xs, void *pout, float *hp, float *out,
                            int K, int O, int rcap, int rmax, int act, float act_a, float act_b,
-                           hipStream_t st) {
+                           hipStream_t st, const int *dest, const float *wrow) {
     if (n_items <= 0)
         return hipSuccess;
     if ((tpw == 2 && ks != 1) || (tpw != 1 && tpw != 2) || K > kDecMaxK ||
@@ -547,6 +554,8 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const
     a.pout = static_cast<__bf16 *>(pout);
     a.hp = hp;
     a.out = out;
+    a.dest = dest;
+    a.wrow = wrow;
     a.K = K;
     a.O = O;
     a.rcap = rcap;

@@ -69,7 +69,9 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
 // split 1, 2 or 4; tpw = tiles per wave 1 or 2, 2 only with ks 1).  Requires fmt 4/7,
 // K % 1024 == 0, K <= kDecMaxK, K / ks <= 2048 (fmt 4) or 4096 (fmt 7), O % 1024 == 0,
 // 16-byte aligned weights, 4-byte aligned scales, 16-byte aligned input rows, LDS
-// (mfma_dec_lds_bytes) <= kDecLdsBudget and staging within kDecStage* registers.
+// (mfma_dec_lds_bytes) <= kDecLdsBudget and staging within kDecStage* registers.  With
+// dest/wrow the down kernel folds the top-k combine in: out[dest[j]] += wrow[j] * y_j by
+// float atomics (out = the caller's output, row stride O), and no Y is written.
 constexpr size_t kDecLdsBudget = 163840;
 constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4096)
 constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12288)
@@ -79,7 +81,8 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const
                            const void *items, int n_items, const float *xin, const int *in_rows,
                            const void *pin, const float *xs, void *pout, float *hp, float *out,
                            int K, int O, int rcap, int rmax, int act, float act_a, float act_b,
-                           hipStream_t st);
+                           hipStream_t st, const int *dest = nullptr,
+                           const float *wrow = nullptr);
 
 // Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
 // nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per

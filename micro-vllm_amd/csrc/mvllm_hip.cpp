@@ -140,6 +140,7 @@ struct Ctx {
     int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2 or 4
     int gemm = 0;            // grouped GEMM: 0 auto, 1 whenever it applies, 2 never
     int fp4act = 0;          // MXFP4 experts: 1 = quantize activations, native FP4 GEMMs
+    int combine_ordered = 0;  // 1 = separate combine in the reference's order (decode too)
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -267,6 +268,7 @@ struct CallCfg {
     bool mfma = false;        // decode-shaped matrix-core kernels
     bool gemm = false;        // grouped GEMM (prefill-shaped)
     bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
+    bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
@@ -419,8 +421,12 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
         pick_rmax(fmt, I, cc.terms, false, 1) >= 1) {
         cc.mfma = add_phase(C, cc, cc.gu, P, split, fmt, D, I, true) &&
                   add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
-        if (cc.mfma)
+        if (cc.mfma) {
+            // decode-sized outputs: fold the combine into the down kernel (one launch less);
+            // option combine_ordered keeps the reference's summation order instead
+            cc.atomic_combine = !C.combine_ordered;
             return;
+        }
         cc.items.clear();
     }
     if (gok && C.gemm != 2) {  // decode-shaped call the decode kernels do not fit: keep
@@ -433,8 +439,8 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
 // device pointers into the slot's device buffer.
 struct DevPlan {
     ExpertWork *ew;
-    int *xrow, *tok_ptr, *ent_row, *out_row, *items;
-    float *ent_w;
+    int *xrow, *tok_ptr, *ent_row, *out_row, *items, *rdest;
+    float *ent_w, *rw;
     PlanSlot *slot;
 };
 
@@ -448,7 +454,9 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t b_x = al(P.xrow.size() * 4), b_tp = al(P.tok_ptr.size() * 4);
     const size_t b_er = al(P.ent_row.size() * 4), b_or = al(P.out_row.size() * 4);
     const size_t b_ew2 = al(P.ent_w.size() * 4), b_it = al(cc.items.size() * 4);
-    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it;
+    const size_t R = P.xrow.size();
+    const size_t b_rd = al(R * 4), b_rw = al(R * 4);
+    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw;
     HIP_TRY(s.host.ensure(total));
     HIP_TRY(s.dev.ensure(total));
     char *h = static_cast<char *>(s.host.p);
@@ -467,6 +475,14 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t o_or = put(P.out_row.data(), P.out_row.size() * 4, b_or);
     const size_t o_w = put(P.ent_w.data(), P.ent_w.size() * 4, b_ew2);
     const size_t o_it = put(cc.items.data(), cc.items.size() * 4, b_it);
+    // per compact row: its row of out (through the combine CSR) and its weight
+    int *rdest = reinterpret_cast<int *>(h + o);
+    for (size_t t = 0; t + 1 < P.tok_ptr.size(); ++t)
+        for (int e = P.tok_ptr[t]; e < P.tok_ptr[t + 1]; ++e)
+            rdest[P.ent_row[e]] = P.out_row[t];
+    const size_t o_rd = o;
+    o += b_rd;
+    const size_t o_rw = put(P.w.data(), R * 4, b_rw);
     HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
     char *d = static_cast<char *>(s.dev.p);
     dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
@@ -476,6 +492,8 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.out_row = reinterpret_cast<int *>(d + o_or);
     dp.ent_w = reinterpret_cast<float *>(d + o_w);
     dp.items = reinterpret_cast<int *>(d + o_it);
+    dp.rdest = reinterpret_cast<int *>(d + o_rd);
+    dp.rw = reinterpret_cast<float *>(d + o_rw);
     dp.slot = &s;
     return 1;
 }
@@ -615,8 +633,10 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                                 dp.items + 4 * cc.dn.it0,
                                 static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, nullptr,
                                 C.Ph.p, static_cast<const float *>(C.HP.p), nullptr, nullptr,
-                                static_cast<float *>(C.Y.p), I, D, rcap, cc.dn.rmax, 0, 0.f, 0.f,
-                                st));
+                                cc.atomic_combine ? out : static_cast<float *>(C.Y.p), I, D,
+                                rcap, cc.dn.rmax, 0, 0.f, 0.f, st,
+                                cc.atomic_combine ? dp.rdest : nullptr,
+                                cc.atomic_combine ? dp.rw : nullptr));
         C.stats[14] += 1;
     } else {
         for (int part = 0; part < 2; ++part) {
@@ -642,6 +662,14 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
     }
     if (C.timing)
         HIP_TRY(hipEventRecord(tc.ev[2], st));
+    if (cc.atomic_combine) {  // already folded into the down kernel
+        if (C.timing) {
+            HIP_TRY(hipEventRecord(tc.ev[3], st));
+            C.timed.push_back(tc);
+        }
+        C.stats[1] += static_cast<double>(R);
+        return 1;
+    }
     CombineArgs cb{};
     cb.Y = static_cast<const float *>(C.Y.p);
     cb.tok_ptr = dp.tok_ptr;
@@ -812,6 +840,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return 0;
         C.dec_ks = static_cast<int>(value);
+    } else if (k == "combine_ordered") {
+        C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {
         C.fp4act = value ? 1 : 0;
     } else if (k == "gemm") {

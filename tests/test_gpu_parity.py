@@ -494,3 +494,27 @@ def test_fp4act_config_c4(hip, orc):
     exp = out.copy()
     assert orc.moe_block_fp4act(*c.args(exp), w.act, w.a, w.b) == 1
     _fp4_check(got, exp)
+
+
+@pytest.mark.parametrize("case", [DEV_CASES[1], DEV_CASES[3], DEV_CASES[7], DEV_CASES[-2]])
+def test_combine_ordered_vs_atomic(hip, orc, case):
+    """Decode calls fold the combine into the down kernel (float atomics, any order);
+    option combine_ordered runs the separate combine in the reference's order.  Both meet
+    the decode bar, and rows that receive nothing stay untouched."""
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("combine", case)
+    rng = np.random.default_rng(D * 5 + I + 3)
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    exp = oracle_out(orc, c, act, a, b)
+    got_a = run_dev(hip, c, act, a, b)
+    assert hip.set_option("combine_ordered", 1)
+    try:
+        got_o = run_dev(hip, c, act, a, b)
+    finally:
+        hip.set_option("combine_ordered", 0)
+    for got in (got_a, got_o):
+        assert npref.rel_err(got, exp) < TOL_F32
+    touched = set(int(r) for r in c.rows if 0 <= r < c.S)
+    for t in range(c.out.shape[0]):
+        if t not in touched:
+            assert np.array_equal(got_a[t], c.out[t])
