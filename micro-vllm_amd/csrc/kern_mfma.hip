@@ -36,18 +36,18 @@ namespace mvllm_hip {
 // ---------------------------------------------------------------------------------
 
 // ---------------------------------------------------------------------------------
-// Decode-shaped GEMM.  A workgroup of 16 waves serves one item (up to rmax rows of one
-// expert).  Each wave computes TPW 16-row output tiles of one weight matrix over one of
+// Decode-shaped GEMM.  A workgroup of kDecWaves waves serves one item (up to rmax rows of
+// one expert).  Each wave computes TPW 16-row output tiles of one weight matrix over one of
 // KS equal K ranges: wave w -> tile slot w % TW, matrix (w / TW) % MS, K range
 // w / (TW * MS), with MS = 2 matrices (gate, up) for the dual projection and
-// TW = 16 / (KS * MS) tile slots per workgroup.
+// TW = kDecWaves / (KS * MS) tile slots per workgroup.
 //
 // Memory access.  The weights of a 256-wide K block of a tile (16 rows x 128 bytes) are
 // read with coalesced 8-byte loads -- lane l takes row l / 4, bytes 8 (l % 4) + 32 g of
 // load g -- and moved into the matrix-core layout (lane 16 q + t holds row t, bytes
 // 8 q + 32 g) with ds_bpermute.  A tile's scales over the wave's K range are read once,
 // coalesced, into wave-private LDS.  The item's activations are copied into LDS once for
-// all 16 waves (the dual projection splits the f32 rows into bf16 terms on the way);
+// all waves (the dual projection splits the f32 rows into bf16 terms on the way);
 // those loads are issued before any weight load (vector loads complete in order).  NB
 // blocks per wave stay in flight.  Partial tiles are combined through LDS in fixed order.
 // ---------------------------------------------------------------------------------
@@ -77,7 +77,11 @@ struct DecArgs {
     float act_a, act_b;
 };
 
-constexpr int kDecThreads = 1024;
+#ifndef MVLLM_DEC_NB_EXTRA
+#define MVLLM_DEC_NB_EXTRA 0  // extra weight blocks in flight per wave (tuning)
+#endif
+
+
 constexpr int kScaleDw = 8;  // scale dwords per lane and tile (<= 128 scale bytes per row)
 
 
@@ -109,7 +113,7 @@ __device__ __forceinline__ void compute_block(f4v &acc, bf16x8 (&a)[TERMS][2], c
     for (int g = 0; g < 4; ++g) {
         const int kg = kb + 64 * g;
         // Only the lanes of live rows (t < nrow) read LDS: its bandwidth is shared by the
-        // 16 waves and scales with the active lanes.  `a` is carried across groups and
+        // waves and scales with the active lanes.  `a` is carried across groups and
         // blocks, so the rows past nrow keep the zeros they started with.  The row count
         // goes through an empty asm per group so that the compiler keeps one small masked
         // region per group instead of merging them (register pressure).
@@ -168,14 +172,14 @@ __device__ __forceinline__ void compute_block(f4v &acc, bf16x8 (&a)[TERMS][2], c
             }
         }
         // keep the next group's LDS reads from being hoisted over this one (register
-        // pressure: waves of 1024-thread workgroups have 128 VGPRs each)
+        // pressure: two workgroups share a CU, so each wave has 128 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
     }
 }
 
 // LDS layout of the decode kernel: A rows [rmax][K/8][terms][8] bf16 (+ 16 bytes per
-// row), fmt 4 sums [K/64][16] f32, then the wave-private scales [16 waves][tpw][16][rbw];
-// the combine buffer [16][tpw][4][64] f32 reuses the start.  Returns the total bytes.
+// row), fmt 4 sums [K/64][16] f32, then the wave-private scales [waves][tpw][16][rbw];
+// the combine buffer [waves][tpw][4][64] f32 reuses the start.  Returns the total bytes.
 __host__ __device__ inline int dec_row_bytes(int K, int terms) {
     return K * terms * 2 + 16;  // + 16: consecutive rows start in different LDS banks
 }
@@ -185,8 +189,8 @@ __host__ __device__ inline size_t dec_lds_plan(int fmt, int K, int rmax, int ter
     const size_t planes = (size_t)rmax * dec_row_bytes(K, terms);
     const size_t xs = fmt == 4 ? (size_t)(K / 64) * 16 * 4 : 0;
     const size_t rbw = (size_t)(K / ks) / (fmt == 4 ? 16 : 32);  // scale bytes per tile row
-    const size_t sc = (size_t)16 * tpw * 16 * rbw;
-    const size_t red = (ks > 1 || dual) ? (size_t)16 * tpw * 4 * 64 * 4 : 0;
+    const size_t sc = (size_t)kDecWaves * tpw * 16 * rbw;
+    const size_t red = (ks > 1 || dual) ? (size_t)kDecWaves * tpw * 4 * 64 * 4 : 0;
     if (off_xs)
         *off_xs = planes;
     if (off_sc)
@@ -196,10 +200,11 @@ __host__ __device__ inline size_t dec_lds_plan(int fmt, int K, int rmax, int ter
 }
 
 template <int FMT, bool DUAL, int TERMS, int KS, int TPW, int SR>
-__global__ __launch_bounds__(kDecThreads) void k_mfma_dec(DecArgs A) {
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void k_mfma_dec(DecArgs A) {
     constexpr int MS = DUAL ? 2 : 1;
-    constexpr int TW = 16 / (KS * MS);  // tile slots per workgroup
-    constexpr int NB = (TERMS == 1 && TPW == 1) ? 4 : 3;  // blocks in flight (VGPR budget)
+    constexpr int TW = kDecWaves / (KS * MS);  // tile slots per workgroup
+    constexpr int NB = ((TERMS == 1 && TPW == 1) ? 4 : 3) + MVLLM_DEC_NB_EXTRA;  // blocks in flight (VGPR budget)
     constexpr int XSR = 2;              // single, fmt 4: sums per thread (K / 4 <= 2048)
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int item = blockIdx.x / A.wgs;
@@ -231,7 +236,7 @@ __global__ __launch_bounds__(kDecThreads) void k_mfma_dec(DecArgs A) {
     float *lxs = reinterpret_cast<float *>(smem + off_xs);  // [K/64][16]
     uint8_t *lsc = reinterpret_cast<uint8_t *>(smem + off_sc) +
                    (size_t)wave * TPW * 16 * rbw;           // this wave's [TPW][16][rbw]
-    float *red = reinterpret_cast<float *>(smem);  // [16 waves][TPW][4][64], reuses the planes
+    float *red = reinterpret_cast<float *>(smem);  // [waves][TPW][4][64], reuses the planes
 
     // coalesced weight loads: lane l -> row l / 4 of the tile, bytes 8 (l % 4) (+ 32 g)
     const uint32_t voff_w =
@@ -497,22 +502,28 @@ size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks,
 template <int FMT, bool DUAL, int TERMS, int KS, int TPW>
 static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
     const size_t lds = mfma_dec_lds_bytes(FMT, a.K, a.rmax, TERMS, DUAL, KS, TPW);
-    a.wgs = a.O / (16 * TPW * (16 / (KS * (DUAL ? 2 : 1))));
+    a.wgs = a.O / (16 * TPW * (kDecWaves / (KS * (DUAL ? 2 : 1))));
     const dim3 grid((unsigned)(n_items * a.wgs)), block(kDecThreads);
     // staging registers per thread: dual = 8-float chunks of rmax rows, single = uint4 of
     // TERMS planes of rmax rows
     const size_t need = DUAL ? (size_t)a.rmax * (a.K / 8) : (size_t)TERMS * a.rmax * (a.K / 8);
     const int sr = (int)((need + kDecThreads - 1) / kDecThreads);
-    if (DUAL ? sr <= 2 : sr <= 4) {
-        hipLaunchKernelGGL((k_mfma_dec<FMT, DUAL, TERMS, KS, TPW, DUAL ? 2 : 4>), grid, block,
-                           lds, st, a);
-    } else if (DUAL ? sr <= kDecStageDual : sr <= kDecStageSingle) {
-        hipLaunchKernelGGL((k_mfma_dec<FMT, DUAL, TERMS, KS, TPW,
-                                       DUAL ? kDecStageDual : kDecStageSingle>),
-                           grid, block, lds, st, a);
-    } else {
+    auto go = [&](auto kern) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e == hipSuccess)
+            hipLaunchKernelGGL(kern, grid, block, lds, st, a);
+        return e;
+    };
+    hipError_t e;
+    if (DUAL ? sr <= 2 : sr <= 4)
+        e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, TPW, DUAL ? 2 : 4>);
+    else if (DUAL ? sr <= kDecStageDual : sr <= kDecStageSingle)
+        e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, TPW, DUAL ? kDecStageDual : kDecStageSingle>);
+    else
         return hipErrorInvalidValue;
-    }
+    if (e != hipSuccess)
+        return e;
     return hipGetLastError();
 }
 

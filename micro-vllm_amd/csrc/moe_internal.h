@@ -64,17 +64,23 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
 // (compact row j = input row in_rows[j], or j) and splits them into `terms` bf16 terms
 // in LDS; it writes H as terms planes [terms][rcap][I] (+ fmt 4 per-16-column partial
 // sums hp[I/64][4][rcap]) for the down GEMM, which writes Y [rcap][D] f32.  items: int4
-// records {expert, r0, nrow, 0} with nrow <= rmax (<= 16).  A workgroup of 16 waves
-// covers one item and 16 * tpw / (ks * (dual ? 2 : 1)) output tiles of 16 rows (ks = K
+// records {expert, r0, nrow, 0} with nrow <= rmax (<= 16).  A workgroup of kDecWaves waves
+// covers one item and kDecWaves * tpw / (ks * (dual ? 2 : 1)) output tiles of 16 rows (ks = K
 // split 1, 2 or 4; tpw = tiles per wave 1 or 2, 2 only with ks 1).  Requires fmt 4/7,
 // K % 1024 == 0, K <= kDecMaxK, K / ks <= 2048 (fmt 4) or 4096 (fmt 7), O % 1024 == 0,
 // 16-byte aligned weights, 4-byte aligned scales, 16-byte aligned input rows, LDS
 // (mfma_dec_lds_bytes) <= kDecLdsBudget and staging within kDecStage* registers.  With
 // dest/wrow the down kernel folds the top-k combine in: out[dest[j]] += wrow[j] * y_j by
 // float atomics (out = the caller's output, row stride O), and no Y is written.
-constexpr size_t kDecLdsBudget = 163840;
-constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4096)
-constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12288)
+// Waves per decode workgroup.  Eight waves at <= 128 VGPRs let two workgroups share a CU,
+// so one streams weights while the other is in its prologue (activation staging) or
+// epilogue (cross-wave combine, H stores) -- phases in which a lone workgroup leaves the
+// CU's memory pipe idle.
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = 64 * kDecWaves;
+constexpr size_t kDecLdsBudget = 163840 / 2;  // two workgroups per CU
+constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4 * threads)
+constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12 * threads)
 constexpr int kDecMaxK = 8192;
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int tpw);
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const ExpertWork *ew,

@@ -284,7 +284,7 @@ bool dec_fits(int fmt, int K, int rmax, int terms, bool dual, int ks, int tpw) {
         return false;
     const size_t stage = dual ? (size_t)rmax * (K / 8)
                               : (size_t)terms * rmax * (K / 8);
-    const size_t cap = (size_t)(dual ? kDecStageDual : kDecStageSingle) * 1024;
+    const size_t cap = (size_t)(dual ? kDecStageDual : kDecStageSingle) * kDecThreads;
     return stage <= cap && mfma_dec_lds_bytes(fmt, K, rmax, terms, dual, ks, tpw) <= kDecLdsBudget;
 }
 
@@ -307,10 +307,11 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
     size_t n_items = 0;
     for (const ExpertWork &w : P.ew)
         n_items += (size_t)((w.nrows + ph.rmax - 1) / ph.rmax);
-    // One workgroup (16 waves) fills a CU.  Each wave streams tpw tiles x K/ks of one
-    // matrix; pick the admissible (ks, tpw) minimising rounds x per-wave blocks (+ a fixed
-    // ramp of ~4 blocks per round) over the 256 CUs.
+    // Two workgroups of kDecWaves waves share a CU.  Each wave streams tpw tiles x K/ks of
+    // one matrix; pick the admissible (ks, tpw) minimising rounds x per-wave blocks (+ a
+    // fixed ramp of ~4 blocks per round) over the 256 CUs.
     const size_t tasks = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // waves at ks=tpw=1
+    const size_t slots = 256 * (size_t)(2 * 8 / kDecWaves);           // resident workgroups
     const int opts[4][2] = {{1, 1}, {2, 1}, {4, 1}, {1, 2}};
     double best = 1e30;
     for (const auto &kt : opts) {
@@ -318,8 +319,8 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
             continue;
         if (C.dec_ks && (kt[0] != C.dec_ks || kt[1] != 1))
             continue;
-        const size_t wgs = tasks * (size_t)kt[0] / (16 * (size_t)kt[1]);
-        const double rounds = (double)((wgs + 255) / 256);
+        const size_t wgs = tasks * (size_t)kt[0] / ((size_t)kDecWaves * (size_t)kt[1]);
+        const double rounds = (double)((wgs + slots - 1) / slots);
         const double cost = rounds * ((double)(K / 256) * kt[1] / kt[0] + 4.0);
         if (cost < best - 1e-9) {
             best = cost;
@@ -394,7 +395,7 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
     cc.terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
     bool ok = (fmt == 4 || fmt == 7) && D % 1024 == 0 && I % 1024 == 0 && D <= kDecMaxK &&
               I <= kDecMaxK && aligned(in, 16);
-    // (% 1024 also covers the O % 512 == 0 that 16-wave workgroups of 2-tile waves need)
+    // (% 1024 also covers the O % 256 that workgroups of kDecWaves 2-tile waves need)
     bool gok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && aligned(in, 16);
     const size_t walign = fmt == 7 && C.fp4act ? 16 : 8;  // the FP4 GEMM loads 16-byte rows
     int most = 0;
