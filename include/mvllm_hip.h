@@ -97,6 +97,9 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
  *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
  *   "dec_ks" 0 = automatic; 1, 2 or 4 forces the split of K across waves.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
+ *   "gemm_persist" 1 = the grouped GEMM's HBM-bound row classes run persistent
+ *            workgroups that prefetch the next task's first K step (same sums; slower
+ *            than the default one workgroup per task at current register use).
  * Shapes the matrix-core kernels do not take (fmt 0, D or Iinter not a multiple of
  * 256, misaligned pointers) run an exact f32 kernel instead. */
 int mvllm_hip_set_option(const char *key, long long value);

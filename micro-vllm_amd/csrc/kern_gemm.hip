@@ -41,6 +41,7 @@ struct GemmArgs {
     float *hp;          // dual, int4: H partial sums [O/64][4][rcap]
     float *out;         // single: Y [rcap][O] f32
     int nbn;            // column blocks per item
+    int n_tasks;        // items * nbn
     int K, O, rcap;
     int act;
     float act_a, act_b;
@@ -66,7 +67,22 @@ struct GStep {
     u32x2 s7[FMT == 7 ? 2 : 1];  // MXFP4: scale bytes of the step's 8 blocks, row t
 };
 
-template <int FMT, bool DUAL, int TERMS, int MT>
+// Where one task's operands live: its two weight tiles (buffer resources + this lane's
+// offsets), its activation rows and its output columns.
+template <int FMT>
+struct TaskD {
+    __amdgpu_buffer_rsrc_t rw[2], rs[2];
+    uint32_t vw[2], vs[2];
+    int jbase, nrow, col0;
+};
+
+// Persistent over tasks (PERSIST): workgroup b runs tasks b, b + G, b + 2G, ...
+// (G = gridDim.x) as one stream of K steps.  The loads of the first two steps of task i + 1 are issued
+// during the last two steps of task i (its descriptor is fetched a whole task earlier),
+// so a task's prologue latency and epilogue stores overlap the neighbouring task's
+// streaming.  Without PERSIST (the compute-bound row classes, whose registers are full),
+// or with an odd number of K steps, the host launches one task per workgroup.
+template <int FMT, bool DUAL, int TERMS, int MT, bool PERSIST>
 __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     constexpr int BM = 16 * MT;
     constexpr int PA = MT >= 8 ? 1 : 2;  // activation prefetch distance in K steps
@@ -76,46 +92,52 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     static_assert(ACH * kGemmThreads == TERMS * BM * (kGemmBK / 8), "A staging split");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    const int item = blockIdx.x / A.nbn;
-    const int nb = blockIdx.x - item * A.nbn;
-    const GemmItem it = A.items[item];
-    const ExpertWork &ew = A.ew[it.a];
-    const int K = A.K, O = A.O, nrow = it.nrow, rcap = A.rcap;
-    const int jbase = ew.row0 + it.r0;
+    const int K = A.K, O = A.O, rcap = A.rcap;
+    const int n_tasks = A.n_tasks;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, t = lane & 15, q = lane >> 4;
-    const int col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
     const uint32_t rowb = (uint32_t)(K >> 1);
     const uint32_t srow = (uint32_t)(FMT == 4 ? (K / 64) * 4 : K / 32);
+    const int nk = K / kGemmBK;
 
-    __amdgpu_buffer_rsrc_t rw[2], rs[2];
-    uint32_t vw[2], vs[2];
+    auto make_task = [&] __attribute__((always_inline)) (int task) {
+        TaskD<FMT> d;
+        const int item = task / A.nbn;
+        const int nb = task - item * A.nbn;
+        const GemmItem it = A.items[item];
+        const ExpertWork &ew = A.ew[it.a];
+        d.jbase = ew.row0 + it.r0;
+        d.nrow = it.nrow;
+        d.col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-        const int mi = DUAL ? m : 2;
-        const int trow = DUAL ? col0 : col0 + 16 * m;  // first weight row of tile m
-        rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
-        rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
-        vw[m] = (uint32_t)(trow + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
-        vs[m] = (uint32_t)(trow + t) * srow;
-    }
-    auto load_b = [&] __attribute__((always_inline)) (GStep<FMT> &b, int k) {
+        for (int m = 0; m < 2; ++m) {
+            const int mi = DUAL ? m : 2;
+            const int trow = DUAL ? d.col0 : d.col0 + 16 * m;  // first weight row of tile m
+            d.rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
+            d.rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
+            d.vw[m] = (uint32_t)(trow + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
+            d.vs[m] = (uint32_t)(trow + t) * srow;
+        }
+        return d;
+    };
+
+    auto load_b = [&] __attribute__((always_inline)) (GStep<FMT> &b, const TaskD<FMT> &d, int k) {
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 b.w[m][g] = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw[m], vw[m] + 32 * g,
+                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rw[m], d.vw[m] + 32 * g,
                                                                 (uint32_t)k * 128u, 0));
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             if constexpr (FMT == 4)
                 b.s4[m] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs[m], vs[m], (uint32_t)k * 16u, 0));
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(d.rs[m], d.vs[m], (uint32_t)k * 16u, 0));
             else
                 b.s7[m] = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[m], vs[m], (uint32_t)k * 8u, 0));
+                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rs[m], d.vs[m], (uint32_t)k * 8u, 0));
         }
     };
 
@@ -126,15 +148,15 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         u32x4 v[ACH];  // native vectors: copies of HIP's uint4 struct go through scratch
         float p[4];  // int4: the four partial sums of this thread's (group, row)
     };
-    auto load_a = [&] __attribute__((always_inline)) (AStage &ra, int k) {
+    auto load_a = [&] __attribute__((always_inline)) (AStage &ra, const TaskD<FMT> &d, int k) {
         // unconditional loads (rows past nrow re-read the last row; their results are
         // never stored) keep the loop body free of branches
 #pragma unroll
         for (int u = 0; u < ACH; ++u) {
             const int c = u * kGemmThreads + tid;
-            const int tm = c / (BM * 32), r = min((c >> 5) % BM, nrow - 1), cc = c & 31;
+            const int tm = c / (BM * 32), r = min((c >> 5) % BM, d.nrow - 1), cc = c & 31;
             ra.v[u] = *reinterpret_cast<const u32x4 *>(
-                A.pin + ((size_t)tm * rcap + jbase + r) * (size_t)K + (size_t)k * kGemmBK +
+                A.pin + ((size_t)tm * rcap + d.jbase + r) * (size_t)K + (size_t)k * kGemmBK +
                 8 * cc);
         }
         if constexpr (FMT == 4) {
@@ -142,8 +164,8 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
             // here would wait for these loads, and with them for every load issued
             // before (loads complete in order)
             const int i4 = tid < 4 * BM ? tid : 0;
-            const int g = i4 / BM, r = min(i4 - g * BM, nrow - 1);
-            const float *p = A.xs + (size_t)(4 * k + g) * 4 * rcap + jbase + r;
+            const int g = i4 / BM, r = min(i4 - g * BM, d.nrow - 1);
+            const float *p = A.xs + (size_t)(4 * k + g) * 4 * rcap + d.jbase + r;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 ra.p[i] = p[i * rcap];
@@ -242,82 +264,104 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         }
     };
 
-    // software pipeline: B two steps ahead in registers; A staged into LDS one step
-    // ahead from registers loaded PA steps ahead (PA = 1 for the compute-bound 128-row
-    // class, whose registers are full).  Loads past the last step are harmless and never
-    // consumed (weights: the next rows' bytes or zeros past the buffer; activations: the
-    // step index is clamped), so the body has no branches around its loads; the
-    // scheduling barriers keep each step's uses of a register set ahead of the loads
-    // that refill it (no copies of in-flight registers, no early waits).
-    const int nk = K / kGemmBK;
-    GStep<FMT> b0, b1;
-    AStage ra0, ra1;
-    load_a(ra0, 0);
-    if constexpr (PA == 2)
-        load_a(ra1, min(1, nk - 1));
-    load_b(b0, 0);
-    load_b(b1, 1);
-    store_a(ra0, 0);
-    __syncthreads();
-    for (int k = 0; k < nk; k += 2) {
-        // even step: LDS buffer 0, weights b0; stage A(k + 1) into buffer 1
-        if constexpr (PA == 2)
-            load_a(ra0, min(k + 2, nk - 1));
-        else
-            load_a(ra1, min(k + 1, nk - 1));
-        compute(b0, 0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, k + 2);
-        store_a(ra1, 1);
-        __syncthreads();
-        if (k + 1 >= nk)
-            break;
-        // odd step: LDS buffer 1, weights b1; stage A(k + 2) into buffer 0
-        if constexpr (PA == 2)
-            load_a(ra1, min(k + 3, nk - 1));
-        else
-            load_a(ra0, min(k + 2, nk - 1));
-        compute(b1, 1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, k + 3);
-        store_a(ra0, 0);
-        __syncthreads();
-    }
-
-    // epilogue: C[4 q + i][t] of row tile mt and tile m
+    // epilogue of one task: C[4 q + i][t] of row tile mt and tile m
+    auto epilogue = [&] __attribute__((always_inline)) (const TaskD<FMT> &d) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
+        for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = mt * 16 + 4 * q + i;
-            const int j = jbase + r;
-            if constexpr (DUAL) {
-                const float h = mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
-                __bf16 tt[3];
-                float rep = split_terms<TERMS>(h, tt);
-                const int col = col0 + t;
-                const int pos = (col & ~7) + a_slot<FMT>(col & 7);
-                if (r < nrow) {
+            for (int i = 0; i < 4; ++i) {
+                const int r = mt * 16 + 4 * q + i;
+                const int j = d.jbase + r;
+                if constexpr (DUAL) {
+                    const float h = mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
+                    __bf16 tt[3];
+                    float rep = split_terms<TERMS>(h, tt);
+                    const int col = d.col0 + t;
+                    const int pos = (col & ~7) + a_slot<FMT>(col & 7);
+                    if (r < d.nrow) {
 #pragma unroll
-                    for (int tm = 0; tm < TERMS; ++tm)
-                        A.pout[((size_t)tm * rcap + j) * O + pos] = tt[tm];
-                }
-                if constexpr (FMT == 4) {
-                    rep += __shfl_xor(rep, 1, 16);
-                    rep += __shfl_xor(rep, 2, 16);
-                    rep += __shfl_xor(rep, 4, 16);
-                    rep += __shfl_xor(rep, 8, 16);
-                    const int tile = col0 >> 4;
-                    if (t == 0 && r < nrow)
-                        A.hp[((size_t)(tile >> 2) * 4 + (tile & 3)) * rcap + j] = rep;
-                }
-            } else {
-                if (r < nrow) {
-                    A.out[(size_t)j * O + col0 + t] = acc[mt][0][i];
-                    A.out[(size_t)j * O + col0 + 16 + t] = acc[mt][1][i];
+                        for (int tm = 0; tm < TERMS; ++tm)
+                            A.pout[((size_t)tm * rcap + j) * O + pos] = tt[tm];
+                    }
+                    if constexpr (FMT == 4) {
+                        rep += __shfl_xor(rep, 1, 16);
+                        rep += __shfl_xor(rep, 2, 16);
+                        rep += __shfl_xor(rep, 4, 16);
+                        rep += __shfl_xor(rep, 8, 16);
+                        const int tile = d.col0 >> 4;
+                        if (t == 0 && r < d.nrow)
+                            A.hp[((size_t)(tile >> 2) * 4 + (tile & 3)) * rcap + j] = rep;
+                    }
+                } else {
+                    if (r < d.nrow) {
+                        A.out[(size_t)j * O + d.col0 + t] = acc[mt][0][i];
+                        A.out[(size_t)j * O + d.col0 + 16 + t] = acc[mt][1][i];
+                    }
                 }
             }
+            acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
         }
+    };
+
+    // software pipeline: B two steps ahead in registers; A staged into LDS one step
+    // ahead from registers loaded PA steps ahead (PA = 1 for the compute-bound 128-row
+    // class, whose registers are full).  Prefetches past a task's last step go to the
+    // next task (or, after the last task, re-read harmless bytes that are never
+    // consumed), so the body has no branches around its loads; the scheduling barriers
+    // keep each step's uses of a register set ahead of the loads that refill it.
+    int task = blockIdx.x;
+    if (task >= n_tasks)
+        return;
+    TaskD<FMT> cur = make_task(task);
+    bool has_next = PERSIST && task + (int)gridDim.x < n_tasks;
+    TaskD<FMT> nxt = cur;
+    if (PERSIST && has_next)
+        nxt = make_task(task + (int)gridDim.x);
+    GStep<FMT> b0, b1;
+    AStage ra0, ra1;
+    load_a(ra0, cur, 0);
+    if constexpr (PA == 2)
+        load_a(ra1, cur, min(1, nk - 1));
+    load_b(b0, cur, 0);
+    load_b(b1, cur, 1);
+    store_a(ra0, 0);
+    __syncthreads();
+    for (;;) {
+        for (int k = 0; k < nk; k += 2) {
+            const bool tail = k + 2 >= nk;  // this pair's prefetches belong to the next task
+            const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
+            const int k2 = tail ? k + 2 - nk : k + 2;
+            // even step: LDS buffer 0, weights b0; stage A(k + 1) into buffer 1
+            if constexpr (PA == 2)
+                load_a(ra0, pd, min(k2, nk - 1));
+            else
+                load_a(ra1, cur, min(k + 1, nk - 1));
+            compute(b0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(b0, pd, k2);
+            store_a(ra1, 1);
+            __syncthreads();
+            if (k + 1 >= nk)
+                break;  // odd step count: one task per workgroup
+            // odd step: LDS buffer 1, weights b1; stage A(k + 2) into buffer 0
+            if constexpr (PA == 2)
+                load_a(ra1, pd, min(k2 + 1, nk - 1));
+            else
+                load_a(ra0, pd, min(k2, nk - 1));
+            compute(b1, 1);
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(b1, pd, k2 + 1);
+            store_a(ra0, 0);
+            __syncthreads();
+        }
+        epilogue(cur);
+        if (!PERSIST || !has_next)
+            break;
+        task += (int)gridDim.x;
+        cur = nxt;
+        has_next = task + (int)gridDim.x < n_tasks;
+        if (has_next)
+            nxt = make_task(task + (int)gridDim.x);
     }
 }
 
@@ -365,17 +409,46 @@ __global__ __launch_bounds__(256) void k_prep_planes(const float *x, const int *
 
 // ---- launchers ----------------------------------------------------------------------
 
-template <int FMT, bool DUAL, int TERMS, int MT>
-static hipError_t launch_gemm_t(const GemmArgs &a, int n_items, hipStream_t st) {
+template <int FMT, bool DUAL, int TERMS, int MT, bool PERSIST>
+static hipError_t launch_gemm_p(GemmArgs a, int n_items, hipStream_t st) {
     const size_t lds = gemm_lds_bytes(FMT, TERMS, MT);
-    auto kern = k_gemm<FMT, DUAL, TERMS, MT>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess)
-        return e;
-    hipLaunchKernelGGL(kern, dim3((unsigned)(n_items * a.nbn)), dim3(kGemmThreads), lds, st, a);
+    auto kern = k_gemm<FMT, DUAL, TERMS, MT, PERSIST>;
+    // resident workgroups of this instantiation (queried once per process)
+    static int resident = 0;
+    if (resident == 0) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        int dev = 0, cus = 0, per_cu = 0;
+        if ((e = hipGetDevice(&dev)) != hipSuccess ||
+            (e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) !=
+                hipSuccess ||
+            (e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                 &per_cu, reinterpret_cast<const void *>(kern), kGemmThreads, lds)) != hipSuccess)
+            return e;
+        resident = std::max(1, cus * std::max(1, per_cu));
+    }
+    a.n_tasks = n_items * a.nbn;
+    // persistent (cross-task prefetch) only with an even number of K steps
+    const int grid = PERSIST && (a.K / kGemmBK) % 2 == 0 ? std::min(a.n_tasks, resident)
+                                                         : a.n_tasks;
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kGemmThreads), lds, st, a);
     return hipGetLastError();
 }
+
+static bool g_gemm_persist = false;  // measured slower than independent workgroups
+
+template <int FMT, bool DUAL, int TERMS, int MT>
+static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
+    if constexpr (MT <= 2 && !(TERMS == 2 && MT == 2)) {  // (that one spills)
+        if (g_gemm_persist && (a.K / kGemmBK) % 2 == 0)
+            return launch_gemm_p<FMT, DUAL, TERMS, MT, true>(a, n_items, st);
+    }
+    return launch_gemm_p<FMT, DUAL, TERMS, MT, false>(a, n_items, st);
+}
+
+void gemm_set_persistent(bool on) { g_gemm_persist = on; }
 
 template <int FMT, bool DUAL>
 static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int mt,

@@ -105,6 +105,10 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
                        const void *items, int n_items, const void *pin, const float *xs,
                        void *pout, float *hp, float *out, int K, int O, int rcap, int act,
                        float act_a, float act_b, hipStream_t st);
+// Option "gemm_persist": the HBM-bound row classes (mt <= 2) run persistent workgroups that
+// prefetch across tasks.  Off by default: on c3/c4 it measured 5-6% slower than launching
+// one workgroup per task (several per CU overlap each other's prologues and tails).
+void gemm_set_persistent(bool on);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
                               int K, int rcap, void *planes, float *xs, hipStream_t st);
 

@@ -29,6 +29,25 @@ namespace {
 
 thread_local std::string g_err;
 
+// A miss expert whose six pieces lie in one block from mvllm_hip_host_alloc and span at
+// most their own bytes plus this much (the ExpertStore's blob padding) is staged with one
+// host-to-device copy of the span.
+constexpr size_t kSpanSlack = 4096;
+
+// Pinned blocks handed out by mvllm_hip_host_alloc: base -> bytes.
+std::mutex g_host_mu;
+std::map<uintptr_t, size_t> g_host_blocks;
+
+// True when [lo, hi) lies inside one block of g_host_blocks.
+bool in_one_host_block(const uint8_t *lo, const uint8_t *hi) {
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    auto it = g_host_blocks.upper_bound(reinterpret_cast<uintptr_t>(lo));
+    if (it == g_host_blocks.begin())
+        return false;
+    --it;
+    return reinterpret_cast<uintptr_t>(hi) <= it->first + it->second;
+}
+
 void set_err(const std::string &s) { g_err = s; }
 
 #define HIP_TRY(expr)                                                                         \
@@ -841,6 +860,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4)
             return 0;
         C.dec_ks = static_cast<int>(value);
+    } else if (k == "gemm_persist") {
+        gemm_set_persistent(value != 0);
     } else if (k == "combine_ordered") {
         C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {
@@ -965,10 +986,11 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
         }
     }
     // 2) misses: copy their pieces on the copy stream into the arena
-    size_t per_expert = 0;
+    size_t per_expert = 0;  // arena bytes per miss: six padded pieces, or one span
     for (int m = 0; m < 3; ++m)
         per_expert += ((pb[m == 2 ? 2 : 0] + 255) & ~size_t(255)) +
                       (fmt ? ((pb[m == 2 ? 3 : 1] + 255) & ~size_t(255)) : 0);
+    per_expert += kSpanSlack + 512;  // a single-span copy may carry slot padding
     hipEvent_t miss_ev = nullptr;
     if (!miss.empty()) {
         HIP_TRY(C.miss.ensure(per_expert * miss.size()));
@@ -978,6 +1000,38 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
         if (C.have_last)
             HIP_TRY(hipStreamWaitEvent(C.copy, C.last_done, 0));
         for (ExpertWork &w : miss) {
+            // the six pieces of an ExpertStore blob are one contiguous host range: one copy
+            // (whole-blob DMA runs closer to the PCIe rate than six small ones)
+            const uint8_t *lo = nullptr, *hi = nullptr;
+            for (int m = 0; m < 3; ++m) {
+                const uint8_t *pw = static_cast<const uint8_t *>(w.w[m]);
+                const size_t bw = pb[m == 2 ? 2 : 0], bs = pb[m == 2 ? 3 : 1];
+                lo = (!lo || pw < lo) ? pw : lo;
+                hi = (!hi || pw + bw > hi) ? pw + bw : hi;
+                if (fmt) {
+                    const uint8_t *ps = static_cast<const uint8_t *>(w.s[m]);
+                    lo = ps < lo ? ps : lo;
+                    hi = ps + bs > hi ? ps + bs : hi;
+                }
+            }
+            size_t pieces = 0;
+            for (int m = 0; m < 3; ++m)
+                pieces += pb[m == 2 ? 2 : 0] + (fmt ? pb[m == 2 ? 3 : 1] : 0);
+            // start at the 256-byte boundary below (blocks are page aligned): the device copy
+            // then keeps every piece's alignment
+            lo = reinterpret_cast<const uint8_t *>(reinterpret_cast<uintptr_t>(lo) & ~uintptr_t(255));
+            if ((size_t)(hi - lo) <= pieces + kSpanSlack && in_one_host_block(lo, hi)) {
+                const size_t span = (size_t)(hi - lo);
+                HIP_TRY(hipMemcpyAsync(arena + off, lo, span, hipMemcpyHostToDevice, C.copy));
+                for (int m = 0; m < 3; ++m) {
+                    w.w[m] = arena + off + (static_cast<const uint8_t *>(w.w[m]) - lo);
+                    if (fmt)
+                        w.s[m] = arena + off + (static_cast<const uint8_t *>(w.s[m]) - lo);
+                }
+                off += (span + 255) & ~size_t(255);
+                C.stats[2] += static_cast<double>(span);
+                continue;
+            }
             for (int m = 0; m < 3; ++m) {
                 const size_t bw = pb[m == 2 ? 2 : 0], bs = pb[m == 2 ? 3 : 1];
                 HIP_TRY(hipMemcpyAsync(arena + off, w.w[m], bw, hipMemcpyHostToDevice, C.copy));
@@ -1055,12 +1109,19 @@ void *mvllm_hip_host_alloc(size_t bytes) {
         set_err("hipHostMalloc failed");
         return nullptr;
     }
+    std::lock_guard<std::mutex> lk(g_host_mu);
+    g_host_blocks[reinterpret_cast<uintptr_t>(p)] = bytes;
     return p;
 }
 
 void mvllm_hip_host_free(void *p) {
-    if (p)
-        (void)hipHostFree(p);
+    if (!p)
+        return;
+    {
+        std::lock_guard<std::mutex> lk(g_host_mu);
+        g_host_blocks.erase(reinterpret_cast<uintptr_t>(p));
+    }
+    (void)hipHostFree(p);
 }
 
 int mvllm_hip_set_expert_budget(size_t bytes) {
