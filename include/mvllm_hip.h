@@ -95,8 +95,13 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
  *            same expert outputs); by default decode folds the combine into the down
  *            kernel with float atomics (same products, any summation order).
  *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
- *   "dec_ks" 0 = automatic; 1, 2 or 4 forces the split of K across waves.
+ *   "dec_ks" 0 = automatic; 1, 2, 4 or 8 forces the split of K across waves.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
+ *   "fuse"   1 = decode calls with every expert resident run both projections in one
+ *            cooperative launch: the down tasks stream their weights while the gate/up
+ *            tasks finish and wait on per-expert counters.  0 (default) = two launches,
+ *            measured faster (the cooperative launch and the coherent H stores cost more
+ *            than the overlap gains).  Same arithmetic either way.
  *   "gemm_persist" 1 = the grouped GEMM's HBM-bound row classes run persistent
  *            workgroups that prefetch the next task's first K step (same sums; slower
  *            than the default one workgroup per task at current register use).
@@ -160,8 +165,10 @@ void *mvllm_hip_resident_ptr(int layer, int eid);
  *  6 resident hits        7 misses (copied in)   8 evictions
  *  9 kernel ms gate/up    10 kernel ms down      11 kernel ms combine
  *  12 kernel ms quantize  13 launches gate/up    14 launches down
- * Kernel times are filled only with option "timing"=1.  Returns the count
- * written (<= n). */
+ *  15 launches of both decode projections in one (counted in neither 13 nor 14)
+ *  16 waits of such a launch that gave up (sticky; 0 in a correct run)
+ * Kernel times are filled only with option "timing"=1 (a fused launch counts as
+ * gate/up).  Returns the count written (<= n). */
 int mvllm_hip_stats(double *vals, int n);
 void mvllm_hip_stats_reset(void);
 

@@ -24,7 +24,6 @@
 
 namespace mvllm_hip {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 
 struct F4Item {

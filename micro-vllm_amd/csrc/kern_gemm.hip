@@ -23,7 +23,6 @@
 
 namespace mvllm_hip {
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct GemmItem {
     int a;     // expert index into ExpertWork

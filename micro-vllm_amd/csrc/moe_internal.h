@@ -60,35 +60,63 @@ hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, i
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st, const int *rows_map = nullptr);
 
-// Matrix-core path (kern_mfma.hip).  The gate/up GEMM (dual) reads the f32 input rows
-// (compact row j = input row in_rows[j], or j) and splits them into `terms` bf16 terms
-// in LDS; it writes H as terms planes [terms][rcap][I] (+ fmt 4 per-16-column partial
-// sums hp[I/64][4][rcap]) for the down GEMM, which writes Y [rcap][D] f32.  items: int4
-// records {expert, r0, nrow, 0} with nrow <= rmax (<= 16).  A workgroup of kDecWaves waves
-// covers one item and kDecWaves * tpw / (ks * (dual ? 2 : 1)) output tiles of 16 rows (ks = K
-// split 1, 2 or 4; tpw = tiles per wave 1 or 2, 2 only with ks 1).  Requires fmt 4/7,
-// K % 1024 == 0, K <= kDecMaxK, K / ks <= 2048 (fmt 4) or 4096 (fmt 7), O % 1024 == 0,
-// 16-byte aligned weights, 4-byte aligned scales, 16-byte aligned input rows, LDS
-// (mfma_dec_lds_bytes) <= kDecLdsBudget and staging within kDecStage* registers.  With
-// dest/wrow the down kernel folds the top-k combine in: out[dest[j]] += wrow[j] * y_j by
-// float atomics (out = the caller's output, row stride O), and no Y is written.
-// Waves per decode workgroup.  Eight waves at <= 128 VGPRs let two workgroups share a CU,
-// so one streams weights while the other is in its prologue (activation staging) or
-// epilogue (cross-wave combine, H stores) -- phases in which a lone workgroup leaves the
-// CU's memory pipe idle.
+// Matrix-core decode path (kern_mfma.hip).  One descriptor per item (up to rmax <= 16
+// rows of one expert), built by the host: everything a workgroup needs before its first
+// weight load, so one dependent read starts both the weight stream and the activation
+// staging.
+struct DecDesc {
+    const void *w[2];  // the wave's two weight streams: gate and up (dual), down twice
+    const void *s[2];  // their scales (int4: f32 [O][K/64]; MXFP4: ue8m0 [O][K/32])
+    int jbase;         // first compact row of the item (row of H / Y)
+    int nrow;          // rows in the item
+    int pad0[2];
+    int rows[16];      // dual: input row of item row r; single + fold: row of out
+    float wts[16];     // single + fold: combine weight of item row r
+    int pad1[20];
+};
+static_assert(sizeof(DecDesc) == 256, "DecDesc layout");
+
+// The gate/up kernel (dual) reads the f32 input rows and splits them into `terms` bf16
+// terms in LDS; each wave computes the gate and the up tile of the same 16 columns over
+// K / ks and applies the activation in registers (ks > 1: partial sums meet in LDS).  It
+// writes H as terms planes [terms][rcap][I] (+ fmt 4 per-16-column partial sums
+// hp[I/64][4][rcap]) for the down kernel (single), whose waves compute nt (1 or 2) tiles
+// each and write Y [rcap][D] f32 or, with fold, add wts[r] * y into out[rows[r]] by float
+// atomics (the top-k combine; out has row stride O).  A workgroup of kDecWaves waves covers
+// one item and (kDecWaves / ks) * (dual ? 1 : nt) column tiles of 16.
+// Requires fmt 4/7, K % 512 == 0, K % (256 ks) == 0, O % (16 * that tile count) == 0,
+// K <= kDecMaxK,
+// 16-byte aligned weights and scales (int4) / 8-byte aligned scales (MXFP4), 16-byte
+// aligned input rows and LDS (mfma_dec_lds_bytes) <= kDecLdsBudget.
+// Waves per decode workgroup.  Eight waves at <= 128 VGPRs let two workgroups share a CU.
 constexpr int kDecWaves = 8;
 constexpr int kDecThreads = 64 * kDecWaves;
 constexpr size_t kDecLdsBudget = 163840 / 2;  // two workgroups per CU
 constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4 * threads)
 constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12 * threads)
 constexpr int kDecMaxK = 8192;
-size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int tpw);
-hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int tpw, const ExpertWork *ew,
-                           const void *items, int n_items, const float *xin, const int *in_rows,
-                           const void *pin, const float *xs, void *pout, float *hp, float *out,
-                           int K, int O, int rcap, int rmax, int act, float act_a, float act_b,
-                           hipStream_t st, const int *dest = nullptr,
-                           const float *wrow = nullptr);
+size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt);
+hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
+                           int n_items, const float *xin, const void *pin, const float *xs,
+                           void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
+                           int act, float act_a, float act_b, bool fold, hipStream_t st);
+
+// Both decode projections in one cooperative launch (kern_fused.hip), the down projection
+// folding the combine into out.  Descriptors as for launch_mfma_dec, plus: pad0[0] =
+// expert slot (index of the expert's counter in done) in both phases; down pad0[1] =
+// the value done[slot] reaches once this call's gate/up tasks of the expert are stored
+// (the counters only grow: the caller keeps each slot's running total and adds, per
+// call, the gate/up items of the slot x I / (16 * kDecWaves / ks_gu)).  err is set if a
+// wait gave up (never in a correct run).  Terms 2 only; the kernel variants cover
+// ks_gu in {1, 2, 4, 8}, (ks_dn, nt_dn) in {(1, 2), (1, 1), (2, 1), (4, 1)} and down items
+// of 2 * rmax_dn * I / 8 <= 4 * kDecThreads staged chunks.
+bool fused_supported(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn, int rmax_dn, int I);
+hipError_t launch_mfma_fused(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn,
+                             const DecDesc *gu_desc, int n_gu_items, const DecDesc *dn_desc,
+                             int n_dn_items, const float *xin, void *planes, float *hp,
+                             float *out, int D, int I, int rcap, int rmax_gu, int rmax_dn,
+                             int act, float act_a, float act_b, unsigned *done, int *err,
+                             hipStream_t st);
 
 // Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
 // nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per

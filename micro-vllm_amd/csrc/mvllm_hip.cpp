@@ -156,10 +156,16 @@ struct Ctx {
     int mode = 0;
     int timing = 0;
     int dequant_path = 0;    // mvllm_hip_dequant: 0 f32 decode, 1 matrix-core bf16 decode
-    int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2 or 4
+    int dec_ks = 0;          // K split of the decode GEMM: 0 auto, 1, 2, 4 or 8
     int gemm = 0;            // grouped GEMM: 0 auto, 1 whenever it applies, 2 never
     int fp4act = 0;          // MXFP4 experts: 1 = quantize activations, native FP4 GEMMs
     int combine_ordered = 0;  // 1 = separate combine in the reference's order (decode too)
+    int fuse = 0;            // decode: both projections in one cooperative launch
+    // fused launch: per expert slot, gate/up tasks finished on the device (only grows) and
+    // the host's running total of what was launched; err[0] = a wait gave up
+    DevBuf sync;             // [16] int err + unsigned done[cap]
+    size_t sync_cap = 0;
+    std::vector<unsigned> cum, adds;
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -169,7 +175,7 @@ struct Ctx {
     std::multimap<size_t, void *> free_blocks;     // recycled device blocks by size
     std::vector<std::pair<size_t, void *>> pending_free;
     // stats
-    double stats[15] = {0};
+    double stats[17] = {0};
     std::vector<TimedCall> timed;
 };
 
@@ -193,6 +199,7 @@ struct Plan {
     std::vector<int> tok_ptr, ent_row, out_row;
     std::vector<float> ent_w;
     int nr_max = 0;
+    int D = 0, I = 0;
 };
 
 size_t piece_bytes(int fmt, int piece, int D, int I) {
@@ -212,6 +219,8 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
                 const float *const *us, const float *const *ds, const int *xoff, const int *nr,
                 const int *rows, const float *rw, int S) {
     P = Plan();
+    P.D = D;
+    P.I = Iinter;
     int base = 0;
     for (int e = 0; e < nb; ++e) {
         const int nre = nr[e];
@@ -272,7 +281,7 @@ bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // How one call runs: the matrix-core path for both projections (activation planes,
 // items of up to rmax rows), or the exact element-wise kernels.
 struct PhaseCfg {
-    int rmax = 0, ks = 1, tpw = 1;
+    int rmax = 0, ks = 1, nt = 1;  // rows per item, K split, tiles per wave
     size_t it0 = 0, it_split = 0, it1 = 0;  // item range; [it0, it_split) = experts < split
 };
 
@@ -288,6 +297,7 @@ struct CallCfg {
     bool gemm = false;        // grouped GEMM (prefill-shaped)
     bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
     bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
+    bool fused = false;       // decode kernels: one cooperative launch for both projections
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
@@ -295,23 +305,29 @@ struct CallCfg {
     int n_gcls = 0;
 };
 
-// Largest K / ks whose tile scales fit the kernel's per-lane scale registers.
-int dec_max_kr(int fmt) { return fmt == 4 ? 2048 : 4096; }
-
-bool dec_fits(int fmt, int K, int rmax, int terms, bool dual, int ks, int tpw) {
-    if (K / ks > dec_max_kr(fmt))
+// Does the decode kernel take this phase shape (K split ks, nt tiles per wave)?
+bool dec_fits(int fmt, int K, int O, int rmax, int terms, bool dual, int ks, int nt) {
+    const int tiles_wg = (kDecWaves / ks) * (dual ? 1 : nt);
+    if (K % 512 || K % (256 * ks) || O % (16 * tiles_wg) || (dual && nt != 2) ||
+        (nt == 2 && !dual && ks != 1))
         return false;
     const size_t stage = dual ? (size_t)rmax * (K / 8)
                               : (size_t)terms * rmax * (K / 8);
     const size_t cap = (size_t)(dual ? kDecStageDual : kDecStageSingle) * kDecThreads;
-    return stage <= cap && mfma_dec_lds_bytes(fmt, K, rmax, terms, dual, ks, tpw) <= kDecLdsBudget;
+    (void)fmt;
+    return stage <= cap && mfma_dec_lds_bytes(fmt, K, rmax, terms, dual, ks, nt) <= kDecLdsBudget;
 }
 
-// Largest rows-per-item (<= want) that fits with some (ks, tpw); 0 if none.
-int pick_rmax(int fmt, int K, int terms, bool dual, int want) {
+// (ks, nt) choices of a phase: dual waves always carry a gate and an up tile.
+constexpr int kDecOpts[2][5][2] = {
+    {{1, 2}, {1, 1}, {2, 1}, {4, 1}, {8, 1}},   // single (down)
+    {{1, 2}, {2, 2}, {4, 2}, {8, 2}, {0, 0}}};  // dual (gate/up)
+
+// Largest rows-per-item (<= want) that fits with some (ks, nt); 0 if none.
+int pick_rmax(int fmt, int K, int O, int terms, bool dual, int want) {
     for (int r = std::min(16, want); r > 0; --r)
-        for (int ks : {1, 2, 4})
-            if (dec_fits(fmt, K, r, terms, dual, ks, 1))
+        for (const auto &kt : kDecOpts[dual ? 1 : 0])
+            if (kt[0] && dec_fits(fmt, K, O, r, terms, dual, kt[0], kt[1]))
                 return r;
     return 0;
 }
@@ -322,29 +338,30 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
     int most = 1;
     for (const ExpertWork &w : P.ew)
         most = std::max(most, w.nrows);
-    ph.rmax = pick_rmax(fmt, K, cc.terms, dual, most);
+    ph.rmax = pick_rmax(fmt, K, O, cc.terms, dual, most);
+    if (ph.rmax < 1)
+        return false;
     size_t n_items = 0;
     for (const ExpertWork &w : P.ew)
         n_items += (size_t)((w.nrows + ph.rmax - 1) / ph.rmax);
-    // Two workgroups of kDecWaves waves share a CU.  Each wave streams tpw tiles x K/ks of
-    // one matrix; pick the admissible (ks, tpw) minimising rounds x per-wave blocks (+ a
-    // fixed ramp of ~4 blocks per round) over the 256 CUs.
-    const size_t tasks = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // waves at ks=tpw=1
+    // Two workgroups of kDecWaves waves share a CU.  Each wave streams nt tiles x K/ks;
+    // pick the admissible (ks, nt) minimising rounds x per-wave blocks (+ a fixed ramp of
+    // ~4 blocks per round) over the 256 CUs.
+    const size_t tiles = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // 16-row weight tiles
     const size_t slots = 256 * (size_t)(2 * 8 / kDecWaves);           // resident workgroups
-    const int opts[4][2] = {{1, 1}, {2, 1}, {4, 1}, {1, 2}};
     double best = 1e30;
-    for (const auto &kt : opts) {
-        if (!dec_fits(fmt, K, ph.rmax, cc.terms, dual, kt[0], kt[1]))
+    for (const auto &kt : kDecOpts[dual ? 1 : 0]) {
+        if (!kt[0] || !dec_fits(fmt, K, O, ph.rmax, cc.terms, dual, kt[0], kt[1]))
             continue;
-        if (C.dec_ks && (kt[0] != C.dec_ks || kt[1] != 1))
+        if (C.dec_ks && kt[0] != C.dec_ks)
             continue;
-        const size_t wgs = tasks * (size_t)kt[0] / ((size_t)kDecWaves * (size_t)kt[1]);
+        const size_t wgs = tiles * (size_t)kt[0] / ((size_t)kDecWaves * (size_t)kt[1]);
         const double rounds = (double)((wgs + slots - 1) / slots);
         const double cost = rounds * ((double)(K / 256) * kt[1] / kt[0] + 4.0);
         if (cost < best - 1e-9) {
             best = cost;
             ph.ks = kt[0];
-            ph.tpw = kt[1];
+            ph.nt = kt[1];
         }
     }
     if (best >= 1e30)
@@ -412,16 +429,15 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
     // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2).  The grouped GEMM takes
     // 1 term by default (bf16 activations, the prefill arithmetic) and 2 in mode 1.
     cc.terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
-    bool ok = (fmt == 4 || fmt == 7) && D % 1024 == 0 && I % 1024 == 0 && D <= kDecMaxK &&
+    bool ok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && D <= kDecMaxK &&
               I <= kDecMaxK && aligned(in, 16);
-    // (% 1024 also covers the O % 256 that workgroups of kDecWaves 2-tile waves need)
     bool gok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && aligned(in, 16);
     const size_t walign = fmt == 7 && C.fp4act ? 16 : 8;  // the FP4 GEMM loads 16-byte rows
     int most = 0;
     for (const ExpertWork &w : P.ew) {
         most = std::max(most, w.nrows);
         for (int m = 0; m < 3; ++m) {
-            ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], 4);
+            ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], fmt == 4 ? 16 : 8);
             gok = gok && aligned(w.w[m], walign) && aligned(w.s[m], fmt == 4 ? 16 : 8);
         }
     }
@@ -437,14 +453,18 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
         plan_gemm(cc, P, split, fmt);
         return;
     }
-    if (ok && pick_rmax(fmt, D, cc.terms, true, 1) >= 1 &&
-        pick_rmax(fmt, I, cc.terms, false, 1) >= 1) {
+    if (ok && pick_rmax(fmt, D, I, cc.terms, true, 1) >= 1 &&
+        pick_rmax(fmt, I, D, cc.terms, false, 1) >= 1) {
         cc.mfma = add_phase(C, cc, cc.gu, P, split, fmt, D, I, true) &&
                   add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
         if (cc.mfma) {
             // decode-sized outputs: fold the combine into the down kernel (one launch less);
             // option combine_ordered keeps the reference's summation order instead
             cc.atomic_combine = !C.combine_ordered;
+            // both projections in one launch when every expert is resident at launch time
+            cc.fused = C.fuse && cc.atomic_combine && split >= P.ew.size() &&
+                       fused_supported(fmt, cc.terms, cc.gu.ks, cc.dn.ks, cc.dn.nt,
+                                       cc.dn.rmax, I);
             return;
         }
         cc.items.clear();
@@ -461,10 +481,40 @@ struct DevPlan {
     ExpertWork *ew;
     int *xrow, *tok_ptr, *ent_row, *out_row, *items, *rdest;
     float *ent_w, *rw;
+    DecDesc *gu_desc, *dn_desc;  // decode kernels: one descriptor per item of each phase
     PlanSlot *slot;
 };
 
-int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp) {
+// Decode descriptors of items [i0, i1) of cc.items.  Dual: the expert's gate and up, and
+// the input row of each item row (x row through the compact-row map, or the compact row
+// itself); single: the down matrix and, with the folded combine, each row's out row and
+// weight.
+void build_desc(const Plan &P, const CallCfg &cc, size_t i0, size_t i1, bool dual,
+                bool rows_identity, const int *rdest, DecDesc *d) {
+    for (size_t it = i0; it < i1; ++it, ++d) {
+        std::memset(d, 0, sizeof(DecDesc));
+        const ExpertWork &w = P.ew[cc.items[4 * it]];
+        const int r0 = cc.items[4 * it + 1], nrow = cc.items[4 * it + 2];
+        d->w[0] = dual ? w.w[0] : w.w[2];
+        d->w[1] = dual ? w.w[1] : w.w[2];
+        d->s[0] = dual ? w.s[0] : w.s[2];
+        d->s[1] = dual ? w.s[1] : w.s[2];
+        d->jbase = w.row0 + r0;
+        d->nrow = nrow;
+        for (int r = 0; r < nrow; ++r) {
+            const int j = d->jbase + r;
+            if (dual) {
+                d->rows[r] = rows_identity ? j : P.xrow[j];
+            } else {
+                d->rows[r] = rdest[j];
+                d->wts[r] = P.w[j];
+            }
+        }
+    }
+}
+
+int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp,
+                bool rows_identity) {
     PlanSlot &s = C.slots[C.slot_next];
     C.slot_next = (C.slot_next + 1) % Ctx::kSlots;
     if (s.used)
@@ -476,7 +526,10 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t b_ew2 = al(P.ent_w.size() * 4), b_it = al(cc.items.size() * 4);
     const size_t R = P.xrow.size();
     const size_t b_rd = al(R * 4), b_rw = al(R * 4);
-    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw;
+    const size_t n_gu = cc.mfma ? cc.gu.it1 - cc.gu.it0 : 0;
+    const size_t n_dn = cc.mfma ? cc.dn.it1 - cc.dn.it0 : 0;
+    const size_t b_dg = n_gu * sizeof(DecDesc), b_dd = n_dn * sizeof(DecDesc);
+    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw + b_dg + b_dd;
     HIP_TRY(s.host.ensure(total));
     HIP_TRY(s.dev.ensure(total));
     char *h = static_cast<char *>(s.host.p);
@@ -503,6 +556,39 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t o_rd = o;
     o += b_rd;
     const size_t o_rw = put(P.w.data(), R * 4, b_rw);
+    const size_t o_dg = o, o_dd = o + b_dg;
+    if (cc.fused) {
+        const size_t ne = P.ew.size();
+        if (ne > C.sync_cap) {  // grow: the device counters restart from zero
+            const size_t cap = std::max<size_t>(ne, 256);
+            HIP_TRY(C.sync.ensure(64 + cap * 4));
+            HIP_TRY(hipMemset(C.sync.p, 0, 64 + cap * 4));
+            C.sync_cap = cap;
+            C.cum.assign(cap, 0u);
+        }
+        C.adds.assign(ne, 0u);
+        const unsigned gwgs = (unsigned)(P.I / (16 * (kDecWaves / cc.gu.ks)));
+        for (size_t it = cc.gu.it0; it < cc.gu.it1; ++it)
+            C.adds[cc.items[4 * it]] += gwgs;
+    }
+    if (cc.mfma) {
+        build_desc(P, cc, cc.gu.it0, cc.gu.it1, true, rows_identity, rdest,
+                   reinterpret_cast<DecDesc *>(h + o_dg));
+        build_desc(P, cc, cc.dn.it0, cc.dn.it1, false, rows_identity, rdest,
+                   reinterpret_cast<DecDesc *>(h + o_dd));
+        if (cc.fused) {  // expert slots, and the counts the down tasks wait for
+            DecDesc *g = reinterpret_cast<DecDesc *>(h + o_dg);
+            for (size_t it = cc.gu.it0; it < cc.gu.it1; ++it)
+                g[it - cc.gu.it0].pad0[0] = cc.items[4 * it];
+            DecDesc *d = reinterpret_cast<DecDesc *>(h + o_dd);
+            for (size_t it = cc.dn.it0; it < cc.dn.it1; ++it) {
+                const int slot = cc.items[4 * it];
+                d[it - cc.dn.it0].pad0[0] = slot;
+                d[it - cc.dn.it0].pad0[1] = (int)(C.cum[slot] + C.adds[slot]);
+            }
+        }
+    }
+    o += b_dg + b_dd;
     HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
     char *d = static_cast<char *>(s.dev.p);
     dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
@@ -514,6 +600,8 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.items = reinterpret_cast<int *>(d + o_it);
     dp.rdest = reinterpret_cast<int *>(d + o_rd);
     dp.rw = reinterpret_cast<float *>(d + o_rw);
+    dp.gu_desc = reinterpret_cast<DecDesc *>(d + o_dg);
+    dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
     dp.slot = &s;
     return 1;
 }
@@ -630,6 +718,22 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                                 static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
             C.stats[14] += 1;
         }
+    } else if (cc.fused) {
+        const size_t tb = (size_t)cc.terms * 2;
+        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
+        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
+        char *sy = static_cast<char *>(C.sync.p);
+        HIP_TRY(launch_mfma_fused(fmt, cc.terms, cc.gu.ks, cc.dn.ks, cc.dn.nt, dp.gu_desc,
+                                  static_cast<int>(cc.gu.it1 - cc.gu.it0), dp.dn_desc,
+                                  static_cast<int>(cc.dn.it1 - cc.dn.it0), in, C.Ph.p,
+                                  static_cast<float *>(C.HP.p), out, D, I, rcap, cc.gu.rmax,
+                                  cc.dn.rmax, act, a, b, reinterpret_cast<unsigned *>(sy + 64),
+                                  reinterpret_cast<int *>(sy), st));
+        for (size_t e = 0; e < C.adds.size(); ++e)  // launched: the targets move on
+            C.cum[e] += C.adds[e];
+        C.stats[15] += 1;
+        if (C.timing)
+            HIP_TRY(hipEventRecord(tc.ev[1], st));
     } else if (cc.mfma) {
         const size_t tb = (size_t)cc.terms * 2;
         HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
@@ -641,22 +745,19 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
             if (i1 <= i0)
                 continue;
-            HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.tpw, dp.ew,
-                                    dp.items + 4 * i0, static_cast<int>(i1 - i0), in, in_rows,
+            HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.nt,
+                                    dp.gu_desc + (i0 - cc.gu.it0), static_cast<int>(i1 - i0), in,
                                     nullptr, nullptr, C.Ph.p, static_cast<float *>(C.HP.p),
-                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, st));
+                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, false, st));
             C.stats[13] += 1;
         }
         if (C.timing)
             HIP_TRY(hipEventRecord(tc.ev[1], st));
-        HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.tpw, dp.ew,
-                                dp.items + 4 * cc.dn.it0,
-                                static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, nullptr,
-                                C.Ph.p, static_cast<const float *>(C.HP.p), nullptr, nullptr,
+        HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.nt, dp.dn_desc,
+                                static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, C.Ph.p,
+                                static_cast<const float *>(C.HP.p), nullptr, nullptr,
                                 cc.atomic_combine ? out : static_cast<float *>(C.Y.p), I, D,
-                                rcap, cc.dn.rmax, 0, 0.f, 0.f, st,
-                                cc.atomic_combine ? dp.rdest : nullptr,
-                                cc.atomic_combine ? dp.rw : nullptr));
+                                rcap, cc.dn.rmax, 0, 0.f, 0.f, cc.atomic_combine, st));
         C.stats[14] += 1;
     } else {
         for (int part = 0; part < 2; ++part) {
@@ -817,6 +918,9 @@ void mvllm_hip_shutdown(void) {
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
+    C.sync.release();
+    C.sync_cap = 0;
+    C.cum.clear();
     C.hx.release();
     C.ho.release();
     for (auto &s : C.slots) {
@@ -857,11 +961,13 @@ int mvllm_hip_set_option(const char *key, long long value) {
     } else if (k == "timing") {
         C.timing = value ? 1 : 0;
     } else if (k == "dec_ks") {
-        if (value != 0 && value != 1 && value != 2 && value != 4)
+        if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return 0;
         C.dec_ks = static_cast<int>(value);
     } else if (k == "gemm_persist") {
         gemm_set_persistent(value != 0);
+    } else if (k == "fuse") {
+        C.fuse = value ? 1 : 0;
     } else if (k == "combine_ordered") {
         C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {
@@ -912,7 +1018,7 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
     CallCfg cc;
     plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg);
     DevPlan dp{};
-    if (!upload_plan(C, P, cc, st, dp))
+    if (!upload_plan(C, P, cc, st, dp, false))
         return 0;
     if (!run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
                     P.ew.size(), nullptr))
@@ -1079,7 +1185,7 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     CallCfg cc;
     plan_call(C, cc, P, fmt, D, Iinter, hit.size(), C.Xc.p);
     DevPlan dp{};
-    if (!upload_plan(C, P, cc, st, dp))
+    if (!upload_plan(C, P, cc, st, dp, true))
         return 0;
     const int ok = run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b,
                               static_cast<const float *>(C.Xc.p), nullptr,
@@ -1228,7 +1334,12 @@ int mvllm_hip_stats(double *vals, int n) {
             (void)hipEventDestroy(e);
     }
     C.timed.clear();
-    const int m = std::min(n, 15);
+    if (C.sync.p) {  // waits of the fused launch that gave up (0 in a correct run)
+        int err = 0;
+        if (hipMemcpy(&err, C.sync.p, sizeof(int), hipMemcpyDeviceToHost) == hipSuccess)
+            C.stats[16] = err;
+    }
+    const int m = std::min(n, 17);
     for (int i = 0; i < m; ++i)
         vals[i] = C.stats[i];
     return m;

@@ -535,3 +535,60 @@ def test_combine_ordered_vs_atomic(hip, orc, case):
     for t in range(c.out.shape[0]):
         if t not in touched:
             assert np.array_equal(got_a[t], c.out[t])
+
+
+# ------------------------------------------------------------- fused decode launch
+
+@pytest.mark.parametrize("case", [DEV_CASES[0], DEV_CASES[1], DEV_CASES[2], DEV_CASES[7],
+                                  DEV_CASES[8]])
+def test_fused_vs_two_launches(hip, orc, case):
+    """Option fuse=1: decode calls with every expert resident run both projections in one
+    cooperative launch; the down tasks wait on per-expert counters that the gate/up tasks
+    advance once their H is stored.  Same arithmetic as the two launches (the default);
+    both meet the decode bar and no wait gives up."""
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("fused", case)
+    rng = np.random.default_rng(D * 7 + I + len(nr))
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    exp = oracle_out(orc, c, act, a, b)
+    hip.stats_reset()
+    assert hip.set_option("fuse", 1)
+    try:
+        got_f = run_dev(hip, c, act, a, b)
+    finally:
+        hip.set_option("fuse", 0)
+    st = hip.stats()
+    say("  fused launches", st["launches_fused"])
+    assert st["launches_fused"] == 1  # every case here has a fused-eligible shape
+    got_u = run_dev(hip, c, act, a, b)
+    for got in (got_f, got_u):
+        assert npref.rel_err(got, exp) < TOL_F32
+    assert npref.rel_err(got_f, got_u) < TOL_F32
+    assert hip.stats()["sync_timeouts"] == 0
+
+
+def test_fused_call_sequence(hip, orc):
+    """Calls in a row with changing expert counts -- including more experts than the
+    counters first held (they are reallocated and restart) -- keep every down task
+    waiting for exactly its own call's gate/up tasks."""
+    say("fused sequence")
+    rng = np.random.default_rng(1234)
+    for i, (fmt, nb, S) in enumerate([(4, 3, 2), (7, 9, 4), (4, 300, 64), (4, 5, 3),
+                                      (7, 290, 40), (4, 2, 1)]):
+        nr = list(rng.integers(1, 3, size=nb))
+        c = random_case(rng, fmt, 512, 512, nr, S, 1 if fmt == 4 else 2,
+                        7.0 if fmt == 4 else 4.0, 0.0 if fmt == 4 else 25.0)
+        act, a, b = (1, 7.0, 0.0) if fmt == 4 else (2, 4.0, 25.0)
+        hip.stats_reset()
+        assert hip.set_option("fuse", 1)
+        try:
+            got = run_dev(hip, c, act, a, b)
+        finally:
+            hip.set_option("fuse", 0)
+        st = hip.stats()
+        exp = oracle_out(orc, c, act, a, b)
+        err = npref.rel_err(got, exp)
+        say("  call", i, "nb", nb, "fused", st["launches_fused"], "rel_err", err)
+        assert st["launches_fused"] == 1
+        assert err < TOL_F32
+    assert hip.stats()["sync_timeouts"] == 0
