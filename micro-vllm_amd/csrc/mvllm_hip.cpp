@@ -589,8 +589,15 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
         }
     }
     o += b_dg + b_dd;
-    HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
-    char *d = static_cast<char *>(s.dev.p);
+    // The decode kernels with the folded combine read nothing of the plan but their
+    // descriptors, and those straight from this pinned slot (no copy, no copy launch):
+    // the slot is rewritten only after the call that read it has finished (above).
+    const bool zero_copy = cc.mfma && cc.atomic_combine;
+    char *d = static_cast<char *>(s.host.p);
+    if (!zero_copy) {
+        HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
+        d = static_cast<char *>(s.dev.p);
+    }
     dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
     dp.xrow = reinterpret_cast<int *>(d + o_x);
     dp.tok_ptr = reinterpret_cast<int *>(d + o_tp);
