@@ -187,20 +187,24 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
 
 // LDS layout of the decode kernel: A rows [rmax][K/8][terms][8] bf16 (+ 16 bytes per
 // row), then fmt 4 sums [K/64][16] f32; the K-range combine buffer [waves][nt][4][64] f32
-// reuses the start.  Returns the total bytes.
+// reuses the start; after all of them the item's 16 out rows and 16 combine weights
+// (the descriptor's, read once in the prologue).  Returns the total bytes.
 __host__ __device__ inline int dec_row_bytes(int K, int terms) {
     return K * terms * 2 + 16;  // + 16: consecutive rows start in different LDS banks
 }
 
 __host__ __device__ inline size_t dec_lds_plan(int fmt, int K, int rmax, int terms, int ks,
-                                               int nt, size_t *off_xs) {
+                                               int nt, size_t *off_xs,
+                                               size_t *off_comb = nullptr) {
     const size_t planes = (size_t)rmax * dec_row_bytes(K, terms);
     const size_t xs = fmt == 4 ? (size_t)(K / 64) * 16 * 4 : 0;
     const size_t red = ks > 1 ? (size_t)kDecWaves * nt * 4 * 64 * 4 : 0;
     if (off_xs)
         *off_xs = planes;
-    const size_t tot = planes + xs;
-    return tot > red ? tot : red;
+    const size_t tot = planes + xs > red ? planes + xs : red;
+    if (off_comb)
+        *off_comb = tot;
+    return tot + 128;
 }
 
 // Cross-workgroup hooks of the fused launch (k_mfma_fused).  The per-XCD L2s are not
@@ -260,8 +264,9 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
         vs[n] = (uint32_t)(tile[n] * 16 + t) * srow;
     }
     const int rsb = dec_row_bytes(K, TERMS);  // bytes per A row in LDS
-    size_t off_xs = 0;
-    dec_lds_plan(FMT, K, A.rmax, TERMS, KS, NT, &off_xs);
+    size_t off_xs = 0, off_comb = 0;
+    dec_lds_plan(FMT, K, A.rmax, TERMS, KS, NT, &off_xs, &off_comb);
+    unsigned *lcomb = reinterpret_cast<unsigned *>(smem + off_comb);  // rows[16], wts[16]
     __bf16 *lp = reinterpret_cast<__bf16 *>(smem);
     float *lxs = reinterpret_cast<float *>(smem + off_xs);  // [K/64][16]
     float *red = reinterpret_cast<float *>(smem);           // [waves][NT][4][64]
@@ -277,7 +282,10 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     float4 xv[DUAL ? SR : 1][2];
     u32x4 st[DUAL ? 1 : SR];
     float xsr[XSR];
+    unsigned comb = 0;  // single: word tid % 32 of the descriptor's rows[16] + wts[16]
     auto stage_loads = [&]() __attribute__((always_inline)) {
+    if constexpr (!DUAL)  // unconditional: every lane loads, lanes < 32 keep it
+        comb = reinterpret_cast<const unsigned *>(dd.rows)[tid & 31];
     if constexpr (DUAL) {
         int rr[16];  // the row map, one scalar load; picked below by uniform selects
 #pragma unroll
@@ -440,6 +448,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                     lxs[i] = -8.f * xsr[u];
             }
         }
+        if (tid < 32)
+            lcomb[tid] = comb;
     }
     __syncthreads();
 
@@ -570,13 +580,13 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
             }
         }
     } else {
-        // this lane's rows 4 q + i of out and their weights (descriptor, read here rather
-        // than held across the loop)
+        // this lane's rows 4 q + i of out and their weights (staged in LDS by the
+        // prologue: the descriptor may live in host memory, too far to read at the end)
         u32x4 drow4 = {0u, 0u, 0u, 0u};
         f4v dwt4 = {0.f, 0.f, 0.f, 0.f};
         if (A.fold) {
-            drow4 = *reinterpret_cast<const u32x4 *>(dd.rows + 4 * q);
-            dwt4 = *reinterpret_cast<const f4v *>(dd.wts + 4 * q);
+            drow4 = *reinterpret_cast<const u32x4 *>(lcomb + 4 * q);
+            dwt4 = *reinterpret_cast<const f4v *>(lcomb + 16 + 4 * q);
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
