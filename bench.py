@@ -81,6 +81,11 @@ def main():
     ap.add_argument("--pool-gb", type=float, default=4.5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe-sizes", action="store_true",
+                    help="also time the stream-read probe at launch-sized reads (8 MiB .. "
+                         "1 GiB, each repetition at a new offset of the pool, so no read is "
+                         "served by the Infinity Cache): the floor one launch of that many "
+                         "bytes can reach")
     ap.add_argument("--staged", type=float, default=None, metavar="MISS_RATE",
                     help="drop-in host entry with the HBM expert tier: this fraction of each "
                          "step's experts is not resident and is copied from pinned host "
@@ -205,6 +210,24 @@ def main():
     del dst
     log(f"HBM stream-read probe: {hbm_gbs:.0f} GB/s over {probe_bytes / 2**30:.2f} GiB; "
         f"copy probe {copy_gbs:.0f} GB/s (read + write) over {copy_bytes / 2**30:.2f} GiB")
+    sizes = {}
+    if args.probe_sizes:
+        flat = pool.view(-1)
+        for mib in (8, 16, 32, 64, 128, 192, 256, 512, 1024):
+            nb = mib << 20
+            if nb * 4 > probe_bytes:
+                break
+            ts, offset = [], 0
+            for r in range(20):
+                if offset + nb > probe_bytes:
+                    offset = 0
+                ms = mvllm_hip.membench(0, flat[offset:offset + nb], sink, nb, 0, 1)
+                offset += nb
+                if r >= 4:
+                    ts.append(ms)
+            t = float(np.median(ts))
+            sizes[mib] = {"us": round(t * 1e3, 2), "gbps": round(nb / t / 1e6, 1)}
+            log(f"  read {mib:5d} MiB in one launch: {t*1e3:8.2f} us, {nb / t / 1e6:7.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -231,6 +254,7 @@ def main():
         "weight_gbps": round(wbytes / ms_step / 1e6, 1),
         "hbm_probe_gbps": round(hbm_gbs, 1),
         "hbm_copy_probe_gbps": round(copy_gbs, 1),
+        **({"hbm_probe_by_size_mib": sizes} if sizes else {}),
         "mfma_util": round(flops / (ms_step * 1e-3) /
                            ((FP4_PEAK_TFS if dtype == "mxfp4" else BF16_PEAK_TFS) * 1e12), 5),
         "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),

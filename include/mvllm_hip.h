@@ -194,7 +194,8 @@ int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_de
  * expert weight rows: 2 = 16 rows x 32 B per load (8-byte lanes), 3 = 32 rows x 32 B,
  * 4 = 16 rows x 64 B, 5 = 4 rows x 256 B, 6 = 1 row x 1 KB (16-byte lanes); dst_dev
  * receives a sink word.
- * Runs `reps` times on the backend's stream; *ms_per_rep gets the mean time.  1 ok. */
+ * Runs `reps` times on the backend's stream, after one untimed warm-up pass when
+ * reps > 1 (reps == 1 times a single cold pass); *ms_per_rep gets the mean time.  1 ok. */
 int mvllm_hip_membench(int kind, const void *src_dev, void *dst_dev, size_t bytes, int row_bytes,
                        int reps, double *ms_per_rep);
 

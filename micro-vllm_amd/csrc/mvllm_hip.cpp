@@ -1410,7 +1410,8 @@ int mvllm_hip_membench(int kind, const void *src_dev, void *dst_dev, size_t byte
     hipEvent_t e0, e1;
     HIP_TRY(hipEventCreate(&e0));
     HIP_TRY(hipEventCreate(&e1));
-    HIP_TRY(launch_membench(kind, src_dev, dst_dev, bytes, row_bytes / 16, C.own));  // warm-up
+    if (reps > 1)  // untimed warm-up pass (a single repetition is timed cold)
+        HIP_TRY(launch_membench(kind, src_dev, dst_dev, bytes, row_bytes / 16, C.own));
     HIP_TRY(hipEventRecord(e0, C.own));
     for (int r = 0; r < reps; ++r)
         HIP_TRY(launch_membench(kind, src_dev, dst_dev, bytes, row_bytes / 16, C.own));
