@@ -143,7 +143,8 @@ hipError_t launch_mfma_fused(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn
         n_dn_items <= 0)
         return hipErrorInvalidValue;
     const int tw_gu = kDecWaves / ks_gu, tw_dn = (kDecWaves / ks_dn) * nt_dn;
-    if (D % 512 || I % 512 || D % (256 * ks_gu) || I % (256 * ks_dn) || I % (16 * tw_gu) ||
+    if (D % 512 || I % 512 || D % (256 * ks_gu) || I % (256 * ks_dn) ||
+        D / ks_gu > dec_max_kr(fmt) || I / ks_dn > dec_max_kr(fmt) || I % (16 * tw_gu) ||
         D % (16 * tw_dn) || rmax_gu < 1 || rmax_gu > 16 || rmax_dn < 1 || rmax_dn > 16)
         return hipErrorInvalidValue;
     const int sg = stage_regs(true, terms, rmax_gu, D);

@@ -27,7 +27,8 @@ template <int FMT, bool DUAL, int TERMS, int KS, int NT>
 static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
     const size_t lds = mfma_dec_lds_bytes(FMT, a.K, a.rmax, TERMS, DUAL, KS, NT);
     const int tiles_wg = (kDecWaves / KS) * (DUAL ? 1 : NT);  // column tiles per workgroup
-    if (a.K % 512 || a.K % (256 * KS) || a.O % (16 * tiles_wg) || a.rmax < 1 || a.rmax > 16 ||
+    if (a.K % 512 || a.K % (256 * KS) || a.K / KS > dec_max_kr(FMT) || a.O % (16 * tiles_wg) ||
+        a.rmax < 1 || a.rmax > 16 ||
         lds > kDecLdsBudget)
         return hipErrorInvalidValue;
     a.wgs = a.O / (16 * tiles_wg);

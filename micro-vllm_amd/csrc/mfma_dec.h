@@ -45,8 +45,8 @@ namespace mvllm_hip {
 // Memory access.  The weights of a 256-wide K block of a tile (16 rows x 128 bytes) come
 // in through coalesced 8-byte loads -- lane l takes row l / 4, bytes 8 (l % 4) + 32 g of
 // load g -- and move into the matrix-core layout (lane 16 q + t holds row t, bytes
-// 8 q + 32 g) with ds_bpermute.  The lanes of row t load that row's scales of the block
-// themselves (int4: 16 bytes = 4 groups; MXFP4: 8 bytes = 8 blocks of 32).  The item's
+// 8 q + 32 g) with ds_bpermute.  A tile's scales over the wave's K range are loaded once
+// (load_scales) and handed out per group by ds_bpermute.  The item's
 // activations are copied into LDS once for all waves (dual: split into bf16 terms on
 // the way).  Their loads are issued first, then the weight loads (vector loads complete
 // in order), both right after the one descriptor read they depend on.  NU K blocks per
@@ -68,33 +68,45 @@ struct DecArgs {
     float act_a, act_b;
 };
 
-// One 256-wide K block of one tile as loaded: weights (lane l: row l / 4) and the
-// scales of row l % 16.
-template <int FMT> struct DBlock;
-template <> struct DBlock<4> {
+// One 256-wide K block of one tile as loaded: lane l holds row l / 4's weight bytes
+// 8 (l % 4) + 32 g, g = 0..3.
+template <int FMT> struct DBlock {
     u32x2 w[4];
-    u32x4 s;  // f32 scales of the block's 4 groups
-};
-template <> struct DBlock<7> {
-    u32x2 w[4];
-    u32x2 s;  // ue8m0 bytes of the block's 8 blocks of 32
 };
 
 template <int FMT>
 __device__ __forceinline__ void load_dblock(DBlock<FMT> &b, __amdgpu_buffer_rsrc_t rw,
-                                            __amdgpu_buffer_rsrc_t rs, uint32_t vw, uint32_t vs,
-                                            int kb) {
+                                            uint32_t vw, int kb) {
     const uint32_t sw = (uint32_t)(kb >> 1);
 #pragma unroll
     for (int g = 0; g < 4; ++g)
         b.w[g] = __builtin_bit_cast(
             u32x2, __builtin_amdgcn_raw_buffer_load_b64(rw, vw + 32 * g, sw, 0));
-    if constexpr (FMT == 4)
-        b.s = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vs, (uint32_t)(kb >> 4), 0));
-    else
-        b.s = __builtin_bit_cast(
-            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs, (uint32_t)(kb >> 5), 0));
+}
+
+// A tile's scales over the wave's whole K range, loaded once: lane (t, q) holds bytes
+// [32 q, 32 q + 32) of row t's scales from the range's start (int4: f32 groups 8 q ..
+// 8 q + 7; MXFP4: ue8m0 bytes of 32-blocks 32 q .. 32 q + 31).  128 bytes a row, hence
+// K / ks <= dec_max_kr.  Reading them per K block instead re-fetched each row's scale
+// line from HBM whenever the L2 had dropped it in between.
+
+template <int FMT>
+__device__ __forceinline__ void load_scales(u32x4 (&sc)[2], __amdgpu_buffer_rsrc_t rs,
+                                            uint32_t vs) {
+    if constexpr (FMT == 4) {  // 16-byte aligned: rows of K / 16 bytes, ranges of 16 * nblk
+        sc[0] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, vs, 0, 0));
+        sc[1] = __builtin_bit_cast(u32x4,
+                                   __builtin_amdgcn_raw_buffer_load_b128(rs, vs + 16, 0, 0));
+    } else {  // 8-byte aligned: rows of K / 32 bytes, ranges of 8 * nblk
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x2 lo = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs + 16 * h, 0, 0));
+            const u32x2 hi = __builtin_bit_cast(
+                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, vs + 16 * h + 8, 0, 0));
+            sc[h] = u32x4{lo.x, lo.y, hi.x, hi.y};
+        }
+    }
 }
 
 // One K block of NT tiles through the matrix cores.  A rows live in LDS as
@@ -106,9 +118,12 @@ __device__ __forceinline__ void load_dblock(DBlock<FMT> &b, __amdgpu_buffer_rsrc
 // of such a wave's tiles) decodes those lanes through decode_b7_exact.
 template <int FMT, int TERMS, int NT, bool EXACT>
 __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS][2],
-                                               const DBlock<FMT> (&b)[NT], const char *tb, int t,
-                                               int nrow, const float *lxs, int kb, int q,
+                                               const DBlock<FMT> (&b)[NT],
+                                               const u32x4 (&sc)[NT][2], int kl, const char *tb,
+                                               int t, int nrow, const float *lxs, int kb, int q,
                                                int src4, bool &exc) {
+    // this block's scale words sit in lane (t, kl / 2) (int4) or (t, kl / 4) (MXFP4)
+    const int ssrc = 4 * (t + 16 * (FMT == 4 ? (kl >> 1) : (kl >> 2)));
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
         // Only the lanes of live rows (t < nrow) read LDS: its bandwidth is shared by the
@@ -134,13 +149,23 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
             // row t's 8 bytes of this group: held by lane 4 t + q of the coalesced load
             const uint32_t wx = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b[n].w[g].x);
             const uint32_t wy = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b[n].w[g].y);
+            // the word of row t holding group g's scale (int4: group 4 kl + g; MXFP4:
+            // 32-blocks 8 kl + 2 g + {0, 1}), picked by a wave-uniform select
+            uint32_t w;
+            if constexpr (FMT == 4) {
+                w = (kl & 1) ? sc[n][1][g] : sc[n][0][g];
+            } else {
+                const int k3 = kl & 3;  // values selected, not references (no stack copy)
+                const uint32_t lo = (k3 & 2) ? sc[n][1][g >> 1] : sc[n][0][g >> 1];
+                const uint32_t hi = (k3 & 2) ? sc[n][1][2 + (g >> 1)] : sc[n][0][2 + (g >> 1)];
+                w = (k3 & 1) ? hi : lo;
+            }
+            const uint32_t sv = (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc, (int)w);
             float sg;
             if constexpr (FMT == 4) {
-                sg = __uint_as_float(b[n].s[g]);
+                sg = __uint_as_float(sv);
             } else {  // lanes q < 2 take 32-block 2 g, q >= 2 block 2 g + 1
-                const uint32_t byte =
-                    (b[n].s[g >> 1] >> (8 * (2 * (g & 1) + (q >> 1)))) & 0xffu;
-                sg = __uint_as_float(byte << 23);
+                sg = __uint_as_float(((sv >> (8 * (2 * (g & 1) + (q >> 1)))) & 0xffu) << 23);
             }
             bf16x8 B0 = decode_b<FMT>(wx, sg);
             bf16x8 B1 = decode_b<FMT>(wy, sg);
@@ -261,7 +286,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
         rw[n] = buf_rsrc(uniform_ptr(dd.w[DUAL ? n : 0]), (uint32_t)O * rowb);
         rs[n] = buf_rsrc(uniform_ptr(dd.s[DUAL ? n : 0]), (uint32_t)O * srow);
         vw[n] = (uint32_t)(tile[n] * 16 + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
-        vs[n] = (uint32_t)(tile[n] * 16 + t) * srow;
+        vs[n] = (uint32_t)(tile[n] * 16 + t) * srow +
+                (uint32_t)(FMT == 4 ? (kw0 >> 4) : (kw0 >> 5)) + 32u * (uint32_t)q;
     }
     const int rsb = dec_row_bytes(K, TERMS);  // bytes per A row in LDS
     size_t off_xs = 0, off_comb = 0;
@@ -356,13 +382,16 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     // make the compiler's wait counts assume none were issued, and the staging below
     // would wait for the weights as well.
     DBlock<FMT> b[NU][NT];
+    u32x4 sc[NT][2];
     auto prefetch = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+            load_scales<FMT>(sc[n], rs[n], vs[n]);
 #pragma unroll
         for (int u = 0; u < NU; ++u)
 #pragma unroll
             for (int n = 0; n < NT; ++n)
-                load_dblock<FMT>(b[u][n], rw[n], rs[n], vw[n], vs[n],
-                                 kw0 + 256 * (u < nblk ? u : nblk - 1));
+                load_dblock<FMT>(b[u][n], rw[n], vw[n], kw0 + 256 * (u < nblk ? u : nblk - 1));
     };
     if constexpr (FUSED && !DUAL) {
         // the weights do not depend on H: stream them while the gate/up tasks finish
@@ -466,13 +495,14 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     bool exc = false;  // MXFP4: this lane met an exceptional scale byte
     auto consume = [&](const DBlock<FMT>(&bb)[NT], int kl) {
         const int kb = kw0 + 256 * kl;
-        compute_dblock<FMT, TERMS, NT, false>(acc, a, bb, ta + (size_t)(kb >> 3) * TERMS * 16,
-                                              t, nrow, lxs, kb, q, src4, exc);
+        compute_dblock<FMT, TERMS, NT, false>(acc, a, bb, sc, kl,
+                                              ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow, lxs,
+                                              kb, q, src4, exc);
     };
     auto reload = [&](DBlock<FMT>(&bb)[NT], int kl) {
 #pragma unroll
         for (int n = 0; n < NT; ++n)
-            load_dblock<FMT>(bb[n], rw[n], rs[n], vw[n], vs[n], kw0 + 256 * kl);
+            load_dblock<FMT>(bb[n], rw[n], vw[n], kw0 + 256 * kl);
     };
     int k0 = 0;
     for (; k0 + 2 * NU <= nblk; k0 += NU) {
@@ -507,7 +537,7 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                 DBlock<FMT> bb[NT];
                 reload(bb, kl);
                 const int kb = kw0 + 256 * kl;
-                compute_dblock<FMT, TERMS, NT, true>(acc, a, bb,
+                compute_dblock<FMT, TERMS, NT, true>(acc, a, bb, sc, kl,
                                                      ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow,
                                                      lxs, kb, q, src4, exc);
             }

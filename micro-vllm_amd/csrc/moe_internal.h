@@ -84,8 +84,8 @@ static_assert(sizeof(DecDesc) == 256, "DecDesc layout");
 // each and write Y [rcap][D] f32 or, with fold, add wts[r] * y into out[rows[r]] by float
 // atomics (the top-k combine; out has row stride O).  A workgroup of kDecWaves waves covers
 // one item and (kDecWaves / ks) * (dual ? 1 : nt) column tiles of 16.
-// Requires fmt 4/7, K % 512 == 0, K % (256 ks) == 0, O % (16 * that tile count) == 0,
-// K <= kDecMaxK,
+// Requires fmt 4/7, K % 512 == 0, K % (256 ks) == 0, K / ks <= dec_max_kr(fmt),
+// O % (16 * that tile count) == 0, K <= kDecMaxK,
 // 16-byte aligned weights and scales (int4) / 8-byte aligned scales (MXFP4), 16-byte
 // aligned input rows and LDS (mfma_dec_lds_bytes) <= kDecLdsBudget.
 // Waves per decode workgroup.  Eight waves at <= 128 VGPRs let two workgroups share a CU.
@@ -95,6 +95,9 @@ constexpr size_t kDecLdsBudget = 163840 / 2;  // two workgroups per CU
 constexpr int kDecStageDual = 4;     // 8-float chunks per thread (rmax * K / 8 <= 4 * threads)
 constexpr int kDecStageSingle = 12;  // uint4 per thread (terms * rmax * K / 8 <= 12 * threads)
 constexpr int kDecMaxK = 8192;
+// Longest K range of one wave: its tiles' scales over the range are held in registers,
+// 128 bytes a row (int4: 32 groups of 64; MXFP4: 128 blocks of 32).
+inline int dec_max_kr(int fmt) { return fmt == 4 ? 2048 : 4096; }
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt);
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,

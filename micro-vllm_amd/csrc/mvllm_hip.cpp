@@ -308,13 +308,12 @@ struct CallCfg {
 // Does the decode kernel take this phase shape (K split ks, nt tiles per wave)?
 bool dec_fits(int fmt, int K, int O, int rmax, int terms, bool dual, int ks, int nt) {
     const int tiles_wg = (kDecWaves / ks) * (dual ? 1 : nt);
-    if (K % 512 || K % (256 * ks) || O % (16 * tiles_wg) || (dual && nt != 2) ||
-        (nt == 2 && !dual && ks != 1))
+    if (K % 512 || K % (256 * ks) || K / ks > dec_max_kr(fmt) || O % (16 * tiles_wg) ||
+        (dual && nt != 2) || (nt == 2 && !dual && ks != 1))
         return false;
     const size_t stage = dual ? (size_t)rmax * (K / 8)
                               : (size_t)terms * rmax * (K / 8);
     const size_t cap = (size_t)(dual ? kDecStageDual : kDecStageSingle) * kDecThreads;
-    (void)fmt;
     return stage <= cap && mfma_dec_lds_bytes(fmt, K, rmax, terms, dual, ks, nt) <= kDecLdsBudget;
 }
 
