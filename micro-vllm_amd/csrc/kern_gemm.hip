@@ -20,6 +20,7 @@
 #include "mfma_common.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mvllm_hip {
 
@@ -35,9 +36,7 @@ struct GemmArgs {
     const ExpertWork *ew;
     const GemmItem *items;
     const __bf16 *pin;  // A planes [TERMS][rcap][K] (int4: 8-blocks in slot order)
-    const float *xs;    // int4: A partial sums [K/64][4][rcap]
     __bf16 *pout;       // dual: H planes [TERMS][rcap][O]
-    float *hp;          // dual, int4: H partial sums [O/64][4][rcap]
     float *out;         // single: Y [rcap][O] f32
     int nbn;            // column blocks per item
     int n_tasks;        // items * nbn
@@ -51,19 +50,29 @@ constexpr int kGemmBK = 256;
 constexpr int kGemmPitch = kGemmBK * 2 + 16;  // LDS bytes per A row and plane (+16: banks)
 
 __host__ __device__ constexpr int gemm_stage_bytes(int fmt, int terms, int mt) {
-    return terms * 16 * mt * kGemmPitch + (fmt == 4 ? 4 * 16 * mt * 4 : 0);
+    return (void)fmt, terms * 16 * mt * kGemmPitch;
 }
 
 size_t gemm_lds_bytes(int fmt, int terms, int mt) {
     return 2 * (size_t)gemm_stage_bytes(fmt, terms, mt);
 }
 
-// Packed weights and scales of one K step for the wave's two tiles, as loaded.
+// Packed weights of one K step for the wave's two tiles, as loaded.
 template <int FMT>
 struct GStep {
     u32x2 w[2][4];
-    u32x4 s4[FMT == 4 ? 2 : 1];  // int4: scales of the step's 4 groups, row t
-    u32x2 s7[FMT == 7 ? 2 : 1];  // MXFP4: scale bytes of the step's 8 blocks, row t
+};
+
+// Scales of one pair of K steps (p = k / 2) for the wave's two tiles, as loaded, each
+// scale once: lane 4 r + c holds row r's int4 group scales 8 p + 2 c and 8 p + 2 c + 1,
+// or its MXFP4 block scale bytes 16 p + 4 c .. 16 p + 4 c + 3.  The compute hands them
+// to the lanes of row r with ds_bpermute.  (Loading each step's scales into every lane of
+// the row took two more 16-row loads per step and their registers; the loop ran 20 %
+// slower for it.)
+template <int FMT>
+struct GScale {
+    u32x2 s4[FMT == 4 ? 2 : 1];
+    uint32_t s7[FMT == 7 ? 2 : 1];
 };
 
 // Where one task's operands live: its two weight tiles (buffer resources + this lane's
@@ -116,7 +125,7 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
             d.rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
             d.rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
             d.vw[m] = (uint32_t)(trow + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
-            d.vs[m] = (uint32_t)(trow + t) * srow;
+            d.vs[m] = (uint32_t)(trow + (lane >> 2)) * srow + (FMT == 4 ? 8u : 4u) * (uint32_t)(lane & 3);
         }
         return d;
     };
@@ -129,23 +138,32 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
                 b.w[m][g] = __builtin_bit_cast(
                     u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rw[m], d.vw[m] + 32 * g,
                                                                 (uint32_t)k * 128u, 0));
+    };
+    // scales of the pair holding step k
+    auto load_s = [&] __attribute__((always_inline)) (GScale<FMT> &s, const TaskD<FMT> &d, int k) {
+        const uint32_t off = (uint32_t)(k >> 1) * (FMT == 4 ? 32u : 16u);
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             if constexpr (FMT == 4)
-                b.s4[m] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(d.rs[m], d.vs[m], (uint32_t)k * 16u, 0));
+                s.s4[m] = __builtin_bit_cast(
+                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rs[m], d.vs[m], off, 0));
             else
-                b.s7[m] = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rs[m], d.vs[m], (uint32_t)k * 8u, 0));
+                s.s7[m] = __builtin_amdgcn_raw_buffer_load_b32(d.rs[m], d.vs[m], off, 0);
         }
     };
+
+    // Set when the fast decode would not reproduce the reference for this task: an MXFP4
+    // scale byte outside the range where the folded bf16 decode is exact
+    // (b7_exceptional), or a non-finite int4 scale (applied to the whole group's sum, where
+    // the reference forms each product (n - 8) * scale).  The task is then computed again
+    // with the exact decode.
+    uint32_t exc = 0;
 
     // A staging: chunk c = u * 512 + tid -> plane c / (BM * 32), row (c / 32) % BM,
     // 16-byte column c % 32 of the step.  Two register sets let the loads of step k + 2
     // be issued while step k computes (PA = 2), so their latency spans two steps.
     struct AStage {
         u32x4 v[ACH];  // native vectors: copies of HIP's uint4 struct go through scratch
-        float p[4];  // int4: the four partial sums of this thread's (group, row)
     };
     auto load_a = [&] __attribute__((always_inline)) (AStage &ra, const TaskD<FMT> &d, int k) {
         // unconditional loads (rows past nrow re-read the last row; their results are
@@ -158,17 +176,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
                 A.pin + ((size_t)tm * rcap + d.jbase + r) * (size_t)K + (size_t)k * kGemmBK +
                 8 * cc);
         }
-        if constexpr (FMT == 4) {
-            // the four partial sums of (group, row) are added only when stored: adding
-            // here would wait for these loads, and with them for every load issued
-            // before (loads complete in order)
-            const int i4 = tid < 4 * BM ? tid : 0;
-            const int g = i4 / BM, r = min(i4 - g * BM, d.nrow - 1);
-            const float *p = A.xs + (size_t)(4 * k + g) * 4 * rcap + d.jbase + r;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                ra.p[i] = p[i * rcap];
-        }
     };
     auto store_a = [&] __attribute__((always_inline)) (const AStage &ra, int buf) {
         char *base = smem + buf * STAGE;
@@ -178,13 +185,6 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
             const int tm = c / (BM * 32), r = (c >> 5) % BM, cc = c & 31;
             *reinterpret_cast<u32x4 *>(base + tm * PL + r * kGemmPitch + cc * 16) = ra.v[u];
         }
-        if constexpr (FMT == 4) {
-            if (tid < 4 * BM) {
-                const int g = tid / BM, r = tid - g * BM;
-                reinterpret_cast<float *>(base + TERMS * PL)[g * BM + r] =
-                    -8.f * (((ra.p[0] + ra.p[1]) + ra.p[2]) + ra.p[3]);
-            }
-        }
     };
 
     f4v acc[MT][2];
@@ -193,34 +193,54 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
         acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
     const int src4 = 4 * (4 * t + q);  // ds_bpermute address of lane 4 t + q
 
-    auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf) {
+
+    // step j (0 or 1) of the pair whose scales are sc
+    auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf,
+                                                         const GScale<FMT> &sc, int j, auto exact) {
+        constexpr bool EXACT = decltype(exact)::value;
         const char *base = smem + buf * STAGE;
-        const float *lsum = reinterpret_cast<const float *>(base + TERMS * PL);
+        // scale words of step j, groups 0-1 / 2-3, sit in lanes 4 t + 2 j and 4 t + 2 j + 1
+        const int ssrc = 4 * (4 * t + 2 * j);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             bf16x8 bf[2][2];
             float sg[2];
+            bool spec[2] = {false, false};  // EXACT int4: this lane's column scale is not finite
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 const uint32_t wx = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].x);
                 const uint32_t wy = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].y);
                 if constexpr (FMT == 4) {
-                    sg[m] = __uint_as_float(b.s4[m][g]);
+                    sg[m] = __uint_as_float((uint32_t)__builtin_amdgcn_ds_bpermute(
+                        ssrc + 4 * (g >> 1), (int)((g & 1) ? sc.s4[m].y : sc.s4[m].x)));
                 } else {  // lanes q < 2 take 32-block 2 g, q >= 2 block 2 g + 1
-                    const int blk = 2 * g + (q >> 1);
-                    const uint32_t word = blk < 4 ? b.s7[m].x : b.s7[m].y;
-                    sg[m] = __uint_as_float(((word >> (8 * (blk & 3))) & 0xffu) << 23);
+                    const uint32_t word =
+                        (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc + 4 * (g >> 1), (int)sc.s7[m]);
+                    const int byte = 2 * (g & 1) + (q >> 1);
+                    sg[m] = __uint_as_float(((word >> (8 * byte)) & 0xffu) << 23);
                 }
-                bf[m][0] = decode_b<FMT>(wx, sg[m]);
-                bf[m][1] = decode_b<FMT>(wy, sg[m]);
-                if constexpr (FMT == 7) {
-                    const bool exc = b7_exceptional(sg[m]);
-                    if (__builtin_expect(__builtin_amdgcn_ballot_w64(exc) != 0, 0)) {
-                        if (exc) {
-                            bf[m][0] = decode_b7_exact(wx, sg[m]);
-                            bf[m][1] = decode_b7_exact(wy, sg[m]);
+                if constexpr (FMT == 7 && EXACT) {
+                    bf[m][0] = decode_b7_exact(wx, sg[m]);
+                    bf[m][1] = decode_b7_exact(wy, sg[m]);
+                } else if constexpr (FMT == 4) {
+                    bf[m][0] = decode_b4_signed(wx);
+                    bf[m][1] = decode_b4_signed(wy);
+                    if constexpr (EXACT) {
+                        // the reference's x * ((n - 8) * scale): a non-finite scale enters
+                        // each product, which then takes the high term of x alone (its
+                        // low terms would turn inf * 0 into NaN)
+                        spec[m] = nonfinite(sg[m]);
+                        if (spec[m]) {
+                            bf[m][0] = mul_bf16x8_exact(bf[m][0], sg[m]);
+                            bf[m][1] = mul_bf16x8_exact(bf[m][1], sg[m]);
                         }
+                    } else {
+                        exc |= (uint32_t)nonfinite(sg[m]);
                     }
+                } else {
+                    bf[m][0] = decode_b<FMT>(wx, sg[m]);
+                    bf[m][1] = decode_b<FMT>(wy, sg[m]);
+                    exc |= (uint32_t)b7_exceptional(sg[m]);
                 }
             }
 #pragma unroll
@@ -233,18 +253,26 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
                     for (int s = 0; s < 2; ++s)
                         a[tm][s] = *reinterpret_cast<const bf16x8 *>(ap + tm * PL + 16 * s);
                 if constexpr (FMT == 4) {
-                    const f4v init = *reinterpret_cast<const f4v *>(lsum + g * BM + mt * 16 + 4 * q);
+                    // each 64-wide group is its own chain over n - 8, then one f32 FMA
+                    // applies the group's scale
 #pragma unroll
                     for (int m = 0; m < 2; ++m) {
-                        f4v c = init;
+                        f4v c = f4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                         for (int tm = 0; tm < TERMS; ++tm) {
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], bf[m][0], c, 0, 0, 0);
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], bf[m][1], c, 0, 0, 0);
+                            bf16x8 b0 = bf[m][0], b1 = bf[m][1];
+                            if (EXACT && tm > 0 && spec[m])
+                                b0 = b1 = bf16x8{};
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], b0, c, 0, 0, 0);
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], b1, c, 0, 0, 0);
                         }
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
-                            acc[mt][m][i] = fmaf(sg[m], c[i], acc[mt][m][i]);
+                            acc[mt][m][i] = EXACT && spec[m] ? acc[mt][m][i] + c[i]
+                                                             : fmaf(sg[m], c[i], acc[mt][m][i]);
+                        // keep the scaling here: sunk below the next step's loads, it
+                        // drags a wait for those loads in with it
+                        asm volatile("" : "+v"(acc[mt][m]));
                     }
                 } else {
 #pragma unroll
@@ -274,22 +302,13 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
                 if constexpr (DUAL) {
                     const float h = mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
                     __bf16 tt[3];
-                    float rep = split_terms<TERMS>(h, tt);
+                    split_terms<TERMS>(h, tt);
                     const int col = d.col0 + t;
                     const int pos = (col & ~7) + a_slot<FMT>(col & 7);
                     if (r < d.nrow) {
 #pragma unroll
                         for (int tm = 0; tm < TERMS; ++tm)
                             A.pout[((size_t)tm * rcap + j) * O + pos] = tt[tm];
-                    }
-                    if constexpr (FMT == 4) {
-                        rep += __shfl_xor(rep, 1, 16);
-                        rep += __shfl_xor(rep, 2, 16);
-                        rep += __shfl_xor(rep, 4, 16);
-                        rep += __shfl_xor(rep, 8, 16);
-                        const int tile = d.col0 >> 4;
-                        if (t == 0 && r < d.nrow)
-                            A.hp[((size_t)(tile >> 2) * 4 + (tile & 3)) * rcap + j] = rep;
                     }
                 } else {
                     if (r < d.nrow) {
@@ -317,41 +336,84 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     if (PERSIST && has_next)
         nxt = make_task(task + (int)gridDim.x);
     GStep<FMT> b0, b1;
+    GScale<FMT> sc, sn;  // scales of this pair of steps / of the next pair
     AStage ra0, ra1;
-    load_a(ra0, cur, 0);
-    if constexpr (PA == 2)
-        load_a(ra1, cur, min(1, nk - 1));
-    load_b(b0, cur, 0);
-    load_b(b1, cur, 1);
-    store_a(ra0, 0);
-    __syncthreads();
+    // The prologue issues its loads in the loop's own order (A, B of step 0, A, B of
+    // step 1): the wait counts at the loop head are merged from both ways in, and a
+    // different order here would make the loop wait for step k + 1's weights too.
+    auto prologue = [&] __attribute__((always_inline)) () {
+        load_a(ra0, cur, 0);
+        load_b(b0, cur, 0);
+        load_s(sn, cur, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PA == 2)
+            load_a(ra1, cur, min(1, nk - 1));
+        load_b(b1, cur, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        store_a(ra0, 0);
+        __syncthreads();
+    };
+    // Even step k: LDS buffer 0, weights b0; stages A(k + 1) into buffer 1.  Prefetches
+    // past the task's last step belong to the next task (PERSIST) or re-read harmless
+    // bytes.
+    auto step_even = [&] __attribute__((always_inline)) (int k, auto exact) {
+        const bool tail = k + 2 >= nk;
+        const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
+        const int k2 = tail ? k + 2 - nk : k + 2;
+        sc = sn;
+        if constexpr (PA == 2)
+            load_a(ra0, pd, min(k2, nk - 1));
+        else
+            load_a(ra1, cur, min(k + 1, nk - 1));
+        compute(b0, 0, sc, 0, exact);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b0, pd, k2);
+        load_s(sn, pd, k2);
+        store_a(ra1, 1);
+        __syncthreads();
+    };
+    // odd step k + 1: LDS buffer 1, weights b1; stages A(k + 2) into buffer 0
+    auto step_odd = [&] __attribute__((always_inline)) (int k, auto exact) {
+        const bool tail = k + 2 >= nk;
+        const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
+        const int k2 = tail ? k + 2 - nk : k + 2;
+        if constexpr (PA == 2)
+            load_a(ra1, pd, min(k2 + 1, nk - 1));
+        else
+            load_a(ra0, pd, min(k2, nk - 1));
+        compute(b1, 1, sc, 1, exact);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(b1, pd, k2 + 1);
+        store_a(ra0, 0);
+        __syncthreads();
+    };
+    // The pair loop has no exit between its two steps: an exit there, merged by the
+    // compiler with the loop test, gives a path from the even step straight back to the
+    // loop head, on which the wait counts would also wait for step k + 1's weights.  An
+    // odd last step runs after the loop.
+    auto k_loop = [&] __attribute__((always_inline)) (auto exact) {
+        for (int k = 0; k + 2 <= nk; k += 2) {
+            step_even(k, exact);
+            step_odd(k, exact);
+        }
+        if (nk & 1)
+            step_even(nk - 1, exact);
+    };
+    prologue();
     for (;;) {
-        for (int k = 0; k < nk; k += 2) {
-            const bool tail = k + 2 >= nk;  // this pair's prefetches belong to the next task
-            const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
-            const int k2 = tail ? k + 2 - nk : k + 2;
-            // even step: LDS buffer 0, weights b0; stage A(k + 1) into buffer 1
-            if constexpr (PA == 2)
-                load_a(ra0, pd, min(k2, nk - 1));
-            else
-                load_a(ra1, cur, min(k + 1, nk - 1));
-            compute(b0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            load_b(b0, pd, k2);
-            store_a(ra1, 1);
-            __syncthreads();
-            if (k + 1 >= nk)
-                break;  // odd step count: one task per workgroup
-            // odd step: LDS buffer 1, weights b1; stage A(k + 2) into buffer 0
-            if constexpr (PA == 2)
-                load_a(ra1, pd, min(k2 + 1, nk - 1));
-            else
-                load_a(ra0, pd, min(k2, nk - 1));
-            compute(b1, 1);
-            __builtin_amdgcn_sched_barrier(0);
-            load_b(b1, pd, k2 + 1);
-            store_a(ra0, 0);
-            __syncthreads();
+        k_loop(std::false_type{});
+        // Rare second pass: some operand of the task needs the exact decode.  The whole
+        // workgroup runs the task again (the A staging is shared); the next task's
+        // prefetches issued by the loop tail are simply issued once more.  (The same loop
+        // with a uniform branch per step instead of this second copy raised the register
+        // count of the common pass.)
+        if (__syncthreads_or((int)exc)) {
+            exc = 0;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+            prologue();
+            k_loop(std::true_type{});
         }
         epilogue(cur);
         if (!PERSIST || !has_next)
@@ -364,45 +426,34 @@ __global__ __launch_bounds__(kGemmThreads) void k_gemm(GemmArgs A) {
     }
 }
 
-// ---- input planes for the GEMM: gather, split into bf16 terms, per-16 partial sums ----
+// ---- input planes for the GEMM: gather, split into bf16 terms ------------------------
 
-// One thread per 8-element chunk of a row; for int4 the two chunks of a 16-column
-// partial sit in adjacent lanes (K / 8 is even).
+// One thread per 8-element chunk of a row.
 template <int FMT, int TERMS>
 __global__ __launch_bounds__(256) void k_prep_planes(const float *x, const int *rows_map, int R,
-                                                     int K, int rcap, __bf16 *planes, float *xs) {
+                                                     int K, int rcap, __bf16 *planes) {
     const int per_row = K >> 3;
     const size_t total = (size_t)R * per_row;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t base = (size_t)blockIdx.x * blockDim.x; base < total; base += stride) {
-        const size_t idx = base + threadIdx.x;
-        const bool ok = idx < total;
-        const int j = ok ? (int)(idx / per_row) : 0;
-        const int c = ok ? (int)(idx - (size_t)j * per_row) : 0;
-        float rs8 = 0.f;
-        if (ok) {
-            const int src = rows_map ? rows_map[j] : j;
-            const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)src * K + 8 * c);
-            const float4 v0 = p[0], v1 = p[1];
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            bf16x8 o[3];
+    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
+        const int j = (int)(idx / per_row);
+        const int c = (int)(idx - (size_t)j * per_row);
+        const int src = rows_map ? rows_map[j] : j;
+        const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)src * K + 8 * c);
+        const float4 v0 = p[0], v1 = p[1];
+        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+        bf16x8 o[3];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                __bf16 tt[3];
-                rs8 += split_terms<TERMS>(v[e], tt);
-#pragma unroll
-                for (int tm = 0; tm < TERMS; ++tm)
-                    o[tm][a_slot<FMT>(e)] = tt[tm];
-            }
+        for (int e = 0; e < 8; ++e) {
+            __bf16 tt[3];
+            split_terms<TERMS>(v[e], tt);
 #pragma unroll
             for (int tm = 0; tm < TERMS; ++tm)
-                *reinterpret_cast<bf16x8 *>(planes + ((size_t)tm * rcap + j) * K + 8 * c) = o[tm];
+                o[tm][a_slot<FMT>(e)] = tt[tm];
         }
-        if constexpr (FMT == 4) {
-            rs8 += __shfl_xor(rs8, 1, 64);
-            if (ok && (c & 1) == 0)
-                xs[((size_t)(c >> 3) * 4 + ((c >> 1) & 3)) * rcap + j] = rs8;
-        }
+#pragma unroll
+        for (int tm = 0; tm < TERMS; ++tm)
+            *reinterpret_cast<bf16x8 *>(planes + ((size_t)tm * rcap + j) * K + 8 * c) = o[tm];
     }
 }
 
@@ -482,8 +533,8 @@ static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int 
 }
 
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
-                       const void *items, int n_items, const void *pin, const float *xs,
-                       void *pout, float *hp, float *out, int K, int O, int rcap, int act,
+                       const void *items, int n_items, const void *pin, void *pout, float *out,
+                       int K, int O, int rcap, int act,
                        float act_a, float act_b, hipStream_t st) {
     if (n_items <= 0)
         return hipSuccess;
@@ -493,9 +544,7 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
     a.ew = ew;
     a.items = static_cast<const GemmItem *>(items);
     a.pin = static_cast<const __bf16 *>(pin);
-    a.xs = xs;
     a.pout = static_cast<__bf16 *>(pout);
-    a.hp = hp;
     a.out = out;
     a.nbn = O / (dual ? 128 : 256);
     a.K = K;
@@ -514,17 +563,17 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
 }
 
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
-                              int K, int rcap, void *planes, float *xs, hipStream_t st) {
+                              int K, int rcap, void *planes, hipStream_t st) {
     if (R <= 0)
         return hipSuccess;
-    if (K % 16)
+    if (K % 8)
         return hipErrorInvalidValue;
     const size_t total = (size_t)R * (K / 8);
     const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
     __bf16 *pl = static_cast<__bf16 *>(planes);
 #define MVLLM_PREP(F, T)                                                                      \
     hipLaunchKernelGGL((k_prep_planes<F, T>), dim3(blocks), dim3(256), 0, st, x, rows_map, R, \
-                       K, rcap, pl, xs)
+                       K, rcap, pl)
     if (fmt == 4) {
         if (terms == 1) MVLLM_PREP(4, 1); else if (terms == 2) MVLLM_PREP(4, 2); else MVLLM_PREP(4, 3);
     } else if (fmt == 7) {

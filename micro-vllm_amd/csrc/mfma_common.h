@@ -43,26 +43,6 @@ __device__ __forceinline__ bf16x8 pack8(bf16x2 a, bf16x2 b, bf16x2 c, bf16x2 d) 
     return r;
 }
 
-__device__ __forceinline__ float mf_mx4_lut(uint32_t n) {
-    const uint32_t e = (n >> 1) & 3u, m = n & 1u;
-    const float mag = e == 0 ? 0.5f * (float)m : (1.f + 0.5f * (float)m) * (float)(1u << (e - 1));
-    return (n & 8u) ? -mag : mag;
-}
-
-// MXFP4 weights whose scale byte e would take lut[n] * 2^(e-127) out of bf16's normal
-// range (e < 2 or e > 252; the reference's e = 0 means +0 and e = 255 means +inf):
-// form the product in f32 as the reference does; it is exactly representable in bf16
-// (or is +-0 / +-inf / NaN), so its high half is the operand.
-__device__ __forceinline__ bf16x8 decode_b7_exact(uint32_t w, float scale7) {
-    bf16x8 r;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float f = mf_mx4_lut((w >> (4 * k)) & 15u) * scale7;
-        r[k] = __builtin_bit_cast(__bf16, (unsigned short)(__float_as_uint(f) >> 16));
-    }
-    return r;
-}
-
 // One dword = 8 weights (K order e0..e7) of one step -> B operand.
 // fmt 4 yields slot order [e0 e2 e4 e6 e1 e3 e5 e7] (the A side is stored permuted to
 // match); fmt 7 yields natural order with the block scale folded in, exact for scale
@@ -81,6 +61,48 @@ __device__ __forceinline__ bf16x8 decode_b(uint32_t w, float scale7) {
                      __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 2),
                      __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale7, 3));
     }
+}
+
+// MXFP4 weights whose scale byte e would take v * 2^(e-127) out of bf16's normal range
+// (e < 2 or e > 252; the reference's e = 0 means +0 and e = 255 means +inf): form the
+// product in f32 as the reference does.  The e2m1 value v converts to bf16 exactly at
+// scale 1; v has at most two significant bits, so v * scale is exact in f32 and in bf16
+// (or is +-0 / +-inf / NaN), and its high half is the operand.
+// v * s per element, formed in f32; exact in bf16 when v has at most 8 significant bits
+// and the product is a power-of-two multiple of v, or +-0 / +-inf / NaN.
+__device__ __forceinline__ bf16x8 mul_bf16x8_exact(bf16x8 v, float s) {
+    bf16x8 r;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float f = (float)v[k] * s;
+        r[k] = __builtin_bit_cast(__bf16, (unsigned short)(__float_as_uint(f) >> 16));
+    }
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 decode_b7_exact(uint32_t w, float scale7) {
+    return mul_bf16x8_exact(decode_b<7>(w, 1.f), scale7);
+}
+
+// int4 nibbles n of one dword -> bf16(n - 8), in decode_b<4>'s slot order, exact: each
+// byte becomes the e4m3 code of (n - 8) * 2^-9 (sign bit and 8 - n for n < 8), which the
+// converter scales back by 2^9.
+__device__ __forceinline__ uint32_t int4_signed_codes(uint32_t l) {  // bytes 0..15
+    const uint32_t ge8 = ((l >> 3) & 0x01010101u) * 0xffu;
+    const uint32_t neg = 0x80808080u | ((~l & 0x07070707u) + 0x01010101u);
+    return (ge8 & (l & 0x07070707u)) | (~ge8 & neg);
+}
+__device__ __forceinline__ bf16x8 decode_b4_signed(uint32_t w) {
+    const int lo = (int)int4_signed_codes(w & 0x0F0F0F0Fu);
+    const int hi = (int)int4_signed_codes((w >> 4) & 0x0F0F0F0Fu);
+    return pack8(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, false),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 512.f, true),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, false),
+                 __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 512.f, true));
+}
+
+__device__ __forceinline__ bool nonfinite(float x) {
+    return (__float_as_uint(x) & 0x7f800000u) == 0x7f800000u;
 }
 
 // Scale bytes the converter does not reproduce: e = 0 (+0 in the reference, 2^-127 in
@@ -106,7 +128,8 @@ __device__ __forceinline__ float split_terms(float x, __bf16 (&t)[3]) {
     t[0] = (__bf16)x;
     float rep = (float)t[0];
     if constexpr (TERMS >= 2) {
-        const float r1 = x - rep;
+        // x = +-inf leaves inf - inf: the high term carries it alone
+        const float r1 = nonfinite(rep) ? 0.f : x - rep;
         t[1] = (__bf16)r1;
         rep += (float)t[1];
         if constexpr (TERMS >= 3) {

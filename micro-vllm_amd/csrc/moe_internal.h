@@ -126,22 +126,22 @@ hipError_t launch_mfma_fused(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn
 // (item, block of 128 columns of each of gate/up, or 256 columns of down).  Requires
 // fmt 4/7, K % 256 == 0, O % 128 (dual) / % 256 (single) == 0, 8-byte aligned weights,
 // 16-byte (int4) / 8-byte (MXFP4) aligned scales and 16-byte aligned planes.  Inputs are
-// the plane format of the decode kernel: [terms][rcap][K] bf16 (+ int4 sums
-// [K/64][4][rcap]); launch_prep_planes builds them from f32 rows.
+// bf16 planes [terms][rcap][K] (int4: K in the 8-block slot order of the decode
+// kernel); launch_prep_planes builds them from f32 rows.
 // Largest row-tile count per workgroup that compiles without spills: int4 carries a
 // per-group chain and scale per row tile, so it stops at 2 tiles (32 rows).
 inline int gemm_max_mt(int fmt, int terms) { return fmt == 4 ? 2 : terms == 1 ? 8 : 4; }
 size_t gemm_lds_bytes(int fmt, int terms, int mt);
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
-                       const void *items, int n_items, const void *pin, const float *xs,
-                       void *pout, float *hp, float *out, int K, int O, int rcap, int act,
-                       float act_a, float act_b, hipStream_t st);
+                       const void *items, int n_items, const void *pin, void *pout, float *out,
+                       int K, int O, int rcap, int act, float act_a, float act_b,
+                       hipStream_t st);
 // Option "gemm_persist": the HBM-bound row classes (mt <= 2) run persistent workgroups that
 // prefetch across tasks.  Off by default: on c3/c4 it measured 5-6% slower than launching
 // one workgroup per task (several per CU overlap each other's prologues and tails).
 void gemm_set_persistent(bool on);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
-                              int K, int rcap, void *planes, float *xs, hipStream_t st);
+                              int K, int rcap, void *planes, hipStream_t st);
 
 // Native MXFP4 GEMM (kern_fp4.hip): v_mfma_scale_f32_16x16x128_f8f6f4 with e2m1 activations
 // (codes [rcap][K/2] + ue8m0 scales [rcap][K/32], from launch_quantize_mxfp4) against the

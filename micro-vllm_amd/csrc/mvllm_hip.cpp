@@ -147,7 +147,7 @@ struct Ctx {
     hipStream_t last_stream = nullptr;
     hipEvent_t last_done = nullptr;  // end of the previous call (any stream)
     bool have_last = false;
-    DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp, XS;
+    DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     HostBuf hx, ho;
     static constexpr int kSlots = 8;
     PlanSlot slots[kSlots];
@@ -696,11 +696,8 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
     } else if (cc.gemm) {
         const size_t tb = (size_t)cc.terms * 2;
         HIP_TRY(C.Xp.ensure(std::max<size_t>(tb * R * D, 256)));
-        HIP_TRY(C.XS.ensure(std::max<size_t>((size_t)(D / 64) * 4 * R * 4, 256)));
         HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
-        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
-        float *xs = static_cast<float *>(C.XS.p), *hp = static_cast<float *>(C.HP.p);
-        HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, C.Xp.p, xs, st));
+        HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, C.Xp.p, st));
         for (int part = 0; part < 2; ++part) {
             if (part == 1 && gate_event)
                 HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
@@ -710,8 +707,8 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 if (i1 <= i0)
                     continue;
                 HIP_TRY(launch_gemm(fmt, true, cc.terms, g.mt, dp.ew, dp.items + 4 * i0,
-                                    static_cast<int>(i1 - i0), C.Xp.p, xs, C.Ph.p, hp, nullptr,
-                                    D, I, rcap, act, a, b, st));
+                                    static_cast<int>(i1 - i0), C.Xp.p, C.Ph.p, nullptr, D, I,
+                                    rcap, act, a, b, st));
                 C.stats[13] += 1;
             }
         }
@@ -720,7 +717,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
             HIP_TRY(launch_gemm(fmt, false, cc.terms, g.mt, dp.ew, dp.items + 4 * g.it0,
-                                static_cast<int>(g.it1 - g.it0), C.Ph.p, hp, nullptr, nullptr,
+                                static_cast<int>(g.it1 - g.it0), C.Ph.p, nullptr,
                                 static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
             C.stats[14] += 1;
         }
@@ -920,7 +917,6 @@ void mvllm_hip_shutdown(void) {
     C.Ph.release();
     C.HP.release();
     C.Xp.release();
-    C.XS.release();
     C.Xc.release();
     C.Oc.release();
     C.miss.release();

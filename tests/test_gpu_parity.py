@@ -433,6 +433,33 @@ def test_gemm_real_shapes(hip, fmt, D, I, nr, act, a, b):
     assert err < TOL_BF16
 
 
+@pytest.mark.parametrize("fmt", [4, 7])
+def test_gemm_nonfinite(hip, orc, fmt):
+    """Nonfinite and out-of-range scales through the grouped GEMM (row classes 1 to 8 for
+    MXFP4): scale bytes 0, 1 and 255 send their task through the exact redo, and NaN and
+    Inf land where the reference puts them."""
+    say("gemm nonfinite", fmt)
+    rng = np.random.default_rng(81 + fmt)
+    nr = [20, 40, 3, 100] if fmt == 7 else [20, 3, 30]
+    c = random_case(rng, fmt, 512, 256, nr, 48, 2 if fmt == 7 else 1, 4.0, 25.0)
+    if fmt == 7:
+        c.gs[0][5, 2] = 255      # +inf scale in one gate group of expert 0
+        c.ds[1][7, 1] = 0        # zero scale in one down group of expert 1
+        c.us[2][3, 0] = 1        # subnormal products in one up group of expert 2
+        c.gs[3][9, 4] = 254      # products up to 6 * 2^127 in one gate group of expert 3
+    else:
+        c.gs[0][5, 1] = np.inf
+        c.ds[1][7, 0] = -np.inf
+    c.xg[25, 17] = np.inf
+    got = _gemm_run(hip, c, 0)
+    exp = oracle_out(orc, c, c.act, c.a, c.b)
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    assert np.array_equal(np.sign(got[np.isinf(exp)]), np.sign(exp[np.isinf(exp)]))
+    fin = np.isfinite(exp)
+    assert npref.rel_err(got[fin], exp[fin]) < TOL_BF16
+
+
 @pytest.mark.parametrize("name,T", [("c3", 16), ("c4", 8)])
 def test_prefill_config_parity(hip, orc, name, T):
     """Prefill configurations at a token count the oracle finishes in seconds, through the
