@@ -113,15 +113,15 @@ __device__ __forceinline__ void load_scales(u32x4 (&sc)[2], __amdgpu_buffer_rsrc
 // [rmax][K/8][TERMS][8] bf16 (a row's terms of each 8-block side by side; tb = this
 // lane's row t at the block's first 8-block plus 2 q; `a` holds zeros for rows
 // t >= nrow); fmt 4 keeps -8 * the per-64 sums of each row as [K/64][16] f32.
-// MXFP4: the common path decodes with the converter and only records in `exc` whether
-// this lane met a scale byte it does not reproduce (b7_exceptional); EXACT (the redo
-// of such a wave's tiles) decodes those lanes through decode_b7_exact.
+// EXACT is the redo of a wave's tiles whose operands the common path does not reproduce
+// (see dec_needs_exact): it decodes per element, MXFP4 through decode_b7_exact, int4 as
+// n - 8 with chains from 0 and a non-finite scale inside each product.
 template <int FMT, int TERMS, int NT, bool EXACT>
 __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS][2],
                                                const DBlock<FMT> (&b)[NT],
                                                const u32x4 (&sc)[NT][2], int kl, const char *tb,
                                                int t, int nrow, const float *lxs, int kb, int q,
-                                               int src4, bool &exc) {
+                                               int src4) {
     // this block's scale words sit in lane (t, kl / 2) (int4) or (t, kl / 4) (MXFP4)
     const int ssrc = 4 * (t + 16 * (FMT == 4 ? (kl >> 1) : (kl >> 2)));
 #pragma unroll
@@ -142,7 +142,7 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
                         tb + (8 * g + s) * TERMS * 16 + tm * 16);
         }
         f4v c0 = {0.f, 0.f, 0.f, 0.f};
-        if constexpr (FMT == 4)
+        if constexpr (FMT == 4 && !EXACT)
             c0 = *reinterpret_cast<const f4v *>(lxs + ((kb >> 6) + g) * 16 + 4 * q);
 #pragma unroll
         for (int n = 0; n < NT; ++n) {
@@ -167,30 +167,45 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
             } else {  // lanes q < 2 take 32-block 2 g, q >= 2 block 2 g + 1
                 sg = __uint_as_float(((sv >> (8 * (2 * (g & 1) + (q >> 1)))) & 0xffu) << 23);
             }
-            bf16x8 B0 = decode_b<FMT>(wx, sg);
-            bf16x8 B1 = decode_b<FMT>(wy, sg);
-            if constexpr (FMT == 7) {
-                if constexpr (EXACT) {
+            bf16x8 B0, B1;
+            bool spec = false;  // EXACT int4: this lane's column scale is not finite
+            if constexpr (FMT == 4 && EXACT) {
+                // the reference's x * ((n - 8) * scale): a non-finite scale enters each
+                // product, which then takes the high term of x alone (its low terms would
+                // turn inf * 0 into NaN)
+                B0 = decode_b4_signed(wx);
+                B1 = decode_b4_signed(wy);
+                spec = nonfinite(sg);
+                if (spec) {
+                    B0 = mul_bf16x8_exact(B0, sg);
+                    B1 = mul_bf16x8_exact(B1, sg);
+                }
+            } else {
+                B0 = decode_b<FMT>(wx, sg);
+                B1 = decode_b<FMT>(wy, sg);
+                if constexpr (FMT == 7 && EXACT) {
                     if (b7_exceptional(sg)) {
                         B0 = decode_b7_exact(wx, sg);
                         B1 = decode_b7_exact(wy, sg);
                     }
-                } else {
-                    exc |= b7_exceptional(sg);
                 }
             }
             if constexpr (FMT == 4) {
                 // the chain starts from -8 * (sum of the group's activations) of each row,
-                // so it ends at sum_k a_k (n_k - 8); one scale per (row, group) then applies
+                // so it ends at sum_k a_k (n_k - 8) (EXACT: n - 8 decoded, from 0); one
+                // scale per (row, group) then applies
                 f4v c = c0;
 #pragma unroll
                 for (int tm = 0; tm < TERMS; ++tm) {
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], B0, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], B1, c, 0, 0, 0);
+                    bf16x8 b0 = B0, b1 = B1;
+                    if (EXACT && tm > 0 && spec)
+                        b0 = b1 = bf16x8{};
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], b0, c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], b1, c, 0, 0, 0);
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[n][i] = fmaf(sg, c[i], acc[n][i]);
+                    acc[n][i] = EXACT && spec ? acc[n][i] + c[i] : fmaf(sg, c[i], acc[n][i]);
                 // materialise acc here: otherwise the chain is sunk past the masked
                 // regions and every group's C and sums stay live to the end of the block
                 asm volatile("" : "+v"(acc[n]));
@@ -208,6 +223,44 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
         // pressure: two workgroups share a CU, so each wave has 128 VGPRs)
         __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// Whether a wave's tiles need the exact redo, checked once after the streaming loop on
+// what the wave holds: its tiles' scales over its K range (sc, this lane's 32 bytes of
+// each row's range; only the nblk blocks' bytes count, as bytes past the scale buffer
+// read as 0) and, for int4, the item's activation sums over the range (xr, [4 nblk][16]
+// f32 in LDS; rows past the item hold 0).  Reasons: an MXFP4 scale byte outside the
+// converter's exact range (b7_exceptional); a non-finite int4 scale (the common path
+// applies it to the group's sum, where the reference forms each product (n - 8) *
+// scale); a non-finite activation (-8 * sum + inf * n is NaN where the reference has
+// +-inf).
+template <int FMT, int NT>
+__device__ __forceinline__ bool dec_needs_exact(const u32x4 (&sc)[NT][2], int q, int nblk,
+                                                const float *xr, int lane) {
+    const int used = (FMT == 4 ? 16 : 8) * nblk;  // scale bytes of a row's range
+    bool r = false;
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (32 * q + 16 * h + 4 * e >= used)
+                    continue;
+                const uint32_t w = sc[n][h][e];
+                if constexpr (FMT == 4) {
+                    r |= nonfinite(__uint_as_float(w));
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        r |= b7_exceptional(__uint_as_float(((w >> (8 * b)) & 0xffu) << 23));
+                }
+            }
+    if constexpr (FMT == 4) {
+        for (int i = lane; i < 64 * nblk; i += 64)
+            r |= nonfinite(xr[i]);
+    }
+    return r;
 }
 
 // LDS layout of the decode kernel: A rows [rmax][K/8][terms][8] bf16 (+ 16 bytes per
@@ -492,12 +545,15 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                      (size_t)(2 * q) * TERMS * 16;
     const int src4 = 4 * (4 * t + q);  // ds_bpermute byte address of lane 4 t + q
     bf16x8 a[TERMS][2] = {};           // A fragments; stay zero in rows t >= nrow
-    bool exc = false;  // MXFP4: this lane met an exceptional scale byte
+    // checked before the loop, while its first weight loads are in flight (the first
+    // block needs the scales anyway); at the end it would lengthen every wave's tail
+    const bool exc = __builtin_amdgcn_ballot_w64(
+                         dec_needs_exact<FMT>(sc, q, nblk, lxs + (kw0 >> 6) * 16, lane)) != 0;
     auto consume = [&](const DBlock<FMT>(&bb)[NT], int kl) {
         const int kb = kw0 + 256 * kl;
         compute_dblock<FMT, TERMS, NT, false>(acc, a, bb, sc, kl,
                                               ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow, lxs,
-                                              kb, q, src4, exc);
+                                              kb, q, src4);
     };
     auto reload = [&](DBlock<FMT>(&bb)[NT], int kl) {
 #pragma unroll
@@ -524,11 +580,11 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     for (int u = 0; u < NU; ++u)
         if (k0 + NU + u < nblk)
             consume(b[u], k0 + NU + u);
-    if constexpr (FMT == 7) {
-        // Rare: scale bytes outside the converter's exact range (e < 2 or e > 252) in
-        // this wave's tiles.  Redo them block by block with the exact decode; the
-        // streaming loop above then carries no exact-path registers.
-        if (__builtin_expect(__builtin_amdgcn_ballot_w64(exc) != 0, 0)) {
+    {
+        // Rare: operands the common path does not reproduce in this wave's tiles.  Redo
+        // the tiles block by block with the exact decode; the streaming loop above then
+        // carries no exact-path registers or checks.
+        if (__builtin_expect(exc, 0)) {
 #pragma unroll
             for (int n = 0; n < NT; ++n)
                 acc[n] = f4v{0.f, 0.f, 0.f, 0.f};
@@ -539,7 +595,7 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                 const int kb = kw0 + 256 * kl;
                 compute_dblock<FMT, TERMS, NT, true>(acc, a, bb, sc, kl,
                                                      ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow,
-                                                     lxs, kb, q, src4, exc);
+                                                     lxs, kb, q, src4);
             }
         }
     }

@@ -215,13 +215,15 @@ def test_validation_matches_reference(hip):
     assert hip.moe_block(*args, 0, 0.0, 0.0) == 1 and np.array_equal(o, c.out)
 
 
-def test_nonfinite_propagation(hip, orc):
-    """Inf scales / activations take the exact per-element path: NaN and Inf land
-    where the reference puts them."""
-    say("nonfinite")
+@pytest.mark.parametrize("D,I", [(256, 128), (512, 512)])
+def test_nonfinite_propagation(hip, orc, D, I):
+    """Inf scales / activations: NaN and Inf land where the reference puts them, on the
+    element-wise path (256 x 128) and through the matrix-core decode kernels (512 x 512:
+    chains over n - 8, exact redo of tiles with out-of-range scales)."""
+    say("nonfinite", D, I)
     rng = np.random.default_rng(8)
     for fmt in (4, 7):
-        c = random_case(rng, fmt, 256, 128, [1, 1, 1], 3, 2 if fmt == 7 else 1, 4.0, 25.0)
+        c = random_case(rng, fmt, D, I, [1, 1, 1], 3, 2 if fmt == 7 else 1, 4.0, 25.0)
         c.rows[:] = [0, 1, 2]
         if fmt == 7:
             c.gs[0][5, 2] = 255      # +inf scale in one gate group of expert 0
