@@ -145,7 +145,9 @@ struct Ctx {
     hipStream_t own = nullptr;   // compute stream for the host-pointer entry
     hipStream_t copy = nullptr;  // promotions / misses
     hipStream_t last_stream = nullptr;
-    hipEvent_t last_done = nullptr;  // end of the previous call (any stream)
+    // end of the previous call (any stream): the event of that call's plan slot, not one
+    // of its own (each event recorded is a queue packet between two calls' kernels)
+    hipEvent_t last_done = nullptr;
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     HostBuf hx, ho;
@@ -623,7 +625,7 @@ int order_after_previous(Ctx &C, hipStream_t st) {
 int finish_call(Ctx &C, hipStream_t st, PlanSlot *slot) {
     HIP_TRY(hipEventRecord(slot->done, st));
     slot->used = true;
-    HIP_TRY(hipEventRecord(C.last_done, st));
+    C.last_done = slot->done;
     C.last_stream = st;
     C.have_last = true;
     return 1;
@@ -656,8 +658,9 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
     const int rcap = static_cast<int>(R);
     TimedCall tc{};
     if (C.timing) {
+        // no system-scope release: its L2 write-back would sit inside the timed spans
         for (auto &e : tc.ev)
-            HIP_TRY(hipEventCreate(&e));
+            HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
         HIP_TRY(hipEventRecord(tc.ev[0], st));
     }
     if (cc.fp4) {
@@ -893,9 +896,12 @@ int mvllm_hip_init(int device) {
     HIP_TRY(hipSetDevice(device));
     HIP_TRY(hipStreamCreateWithFlags(&C.own, hipStreamNonBlocking));
     HIP_TRY(hipStreamCreateWithFlags(&C.copy, hipStreamNonBlocking));
-    HIP_TRY(hipEventCreateWithFlags(&C.last_done, hipEventDisableTiming));
+    // Plan-slot events order the host's reuse of a slot and other streams after a call.
+    // Neither needs the call's device writes visible to the host, so they skip the
+    // system-scope release (an L2 write-back between one call's kernels and the next's).
     for (auto &s : C.slots)
-        HIP_TRY(hipEventCreateWithFlags(&s.done, hipEventDisableTiming));
+        HIP_TRY(hipEventCreateWithFlags(&s.done,
+                                        hipEventDisableTiming | hipEventDisableSystemFence));
     C.device = device;
     C.ready = true;
     return 1;
@@ -936,7 +942,7 @@ void mvllm_hip_shutdown(void) {
         for (auto &e : t.ev)
             (void)hipEventDestroy(e);
     C.timed.clear();
-    (void)hipEventDestroy(C.last_done);
+    C.last_done = nullptr;
     (void)hipStreamDestroy(C.own);
     (void)hipStreamDestroy(C.copy);
     C.have_last = false;
