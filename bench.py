@@ -140,11 +140,12 @@ def main():
     xg = torch.from_numpy(w.xg).cuda()
     out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
     xoff, nr, rows, rw = w.xoff, w.nr, w.rows, w.rw
+    # the same arrays every step: their addresses are looked up once (w keeps them alive)
+    addr = [xg.data_ptr()] + [a.ctypes.data for a in (xoff, nr, rows, rw)] + [out.data_ptr()]
 
     def step(s):
-        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, xg, xoff,
-                                nr, rows, rw, out, T, w.act, w.a, w.b,
-                                prepared=layer_lists[s % layers])
+        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, *addr[:5],
+                                addr[5], T, w.act, w.a, w.b, prepared=layer_lists[s % layers])
 
     for s in range(args.warmup):
         step(s)

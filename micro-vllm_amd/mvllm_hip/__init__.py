@@ -106,8 +106,8 @@ def set_option(key: str, value: int) -> bool:
 
 
 def _ptr(a):
-    if a is None:
-        return None
+    if a is None or isinstance(a, int):  # an address the caller already holds
+        return a
     if isinstance(a, np.ndarray):
         return a.ctypes.data
     return a.data_ptr()  # torch tensor
@@ -139,7 +139,8 @@ def prepare_lists(g, u, d, gs, us, ds):
 def moe_block_dev(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
                   act=ACT_SILU, act_a=0.0, act_b=0.0, stream=None, check=True, prepared=None):
     """Device variant: g..ds are lists of device pointers (ints) or torch tensors;
-    xg/out are torch CUDA tensors; xoff/nr/rows/rw are numpy host arrays.
+    xg/out are torch CUDA tensors; xoff/nr/rows/rw are numpy host arrays.  Any of the
+    arrays may also be given as its address (int), which saves the per-call lookup.
     `prepared` (from prepare_lists) replaces g..ds when given."""
     pa = prepared if prepared is not None else \
         [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
