@@ -66,7 +66,10 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
  * xoff/nr/rows/rw are HOST arrays; the weights and scales they point to, xg
  * ([rows, D] f32) and out ([S, D] f32, accumulated) are DEVICE pointers.
  * Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and the
- * call returns without waiting.  Requires S > 0 (out's row count). */
+ * call returns without waiting.  Requires S > 0 (out's row count).  Calls are ordered
+ * after each other across streams (they share scratch): a call on another stream than
+ * the previous one first marks the previous stream's end, so keep that stream alive
+ * until then (if it is gone, the call drains the device instead). */
 int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
                             const void *const *u, const void *const *d,
                             const float *const *gs, const float *const *us,

@@ -119,8 +119,6 @@ struct HostBuf {
 struct PlanSlot {
     HostBuf host;
     DevBuf dev;
-    hipEvent_t done = nullptr;
-    bool used = false;
 };
 
 struct Resident {
@@ -145,15 +143,21 @@ struct Ctx {
     hipStream_t own = nullptr;   // compute stream for the host-pointer entry
     hipStream_t copy = nullptr;  // promotions / misses
     hipStream_t last_stream = nullptr;
-    // end of the previous call (any stream): the event of that call's plan slot, not one
-    // of its own (each event recorded is a queue packet between two calls' kernels)
-    hipEvent_t last_done = nullptr;
+    // Ordering after the previous call (another stream, the miss copies): recorded on the
+    // previous call's stream when such a call comes, not after every call.  Every event
+    // recorded is a queue packet that idles the GPU between two calls' kernels (~4.6 us).
+    hipEvent_t prev_done = nullptr;
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     HostBuf hx, ho;
-    static constexpr int kSlots = 8;
+    // Plan slots, reused in groups of kGroup: one event after a group's last call guards
+    // the reuse of all its slots.  A group whose last call did not reach finish_call is
+    // drained before its slots are reused (open_last).
+    static constexpr int kSlots = 8, kGroup = 4;
     PlanSlot slots[kSlots];
-    int slot_next = 0;
+    hipEvent_t grp_done[kSlots / kGroup] = {};
+    bool grp_used[kSlots / kGroup] = {};
+    int slot_next = 0, open_last = -1;
     // options
     int mode = 0;
     int timing = 0;
@@ -483,7 +487,7 @@ struct DevPlan {
     int *xrow, *tok_ptr, *ent_row, *out_row, *items, *rdest;
     float *ent_w, *rw;
     DecDesc *gu_desc, *dn_desc;  // decode kernels: one descriptor per item of each phase
-    PlanSlot *slot;
+    int slot;  // plan slot index
 };
 
 // Decode descriptors of items [i0, i1) of cc.items.  Dual: the expert's gate and up, and
@@ -516,10 +520,19 @@ void build_desc(const Plan &P, const CallCfg &cc, size_t i0, size_t i1, bool dua
 
 int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp,
                 bool rows_identity) {
-    PlanSlot &s = C.slots[C.slot_next];
-    C.slot_next = (C.slot_next + 1) % Ctx::kSlots;
-    if (s.used)
-        HIP_TRY(hipEventSynchronize(s.done));  // previous call on this slot is finished
+    if (C.open_last >= 0) {  // a group's last call stopped early: its event is stale
+        HIP_TRY(hipDeviceSynchronize());
+        C.grp_used[C.open_last / Ctx::kGroup] = false;
+        C.open_last = -1;
+    }
+    const int si = C.slot_next;
+    PlanSlot &s = C.slots[si];
+    C.slot_next = (si + 1) % Ctx::kSlots;
+    const int gi = si / Ctx::kGroup;
+    if (si % Ctx::kGroup == 0 && C.grp_used[gi])
+        HIP_TRY(hipEventSynchronize(C.grp_done[gi]));  // the group's previous calls are done
+    if (si % Ctx::kGroup == Ctx::kGroup - 1)
+        C.open_last = si;
     auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
     const size_t b_ew = al(P.ew.size() * sizeof(ExpertWork));
     const size_t b_x = al(P.xrow.size() * 4), b_tp = al(P.tok_ptr.size() * 4);
@@ -610,22 +623,36 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.rw = reinterpret_cast<float *>(d + o_rw);
     dp.gu_desc = reinterpret_cast<DecDesc *>(d + o_dg);
     dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
-    dp.slot = &s;
+    dp.slot = si;
     return 1;
 }
 
 // Scratch H/Y are shared by all calls: order this call after the previous one if it
 // came on another stream.
-int order_after_previous(Ctx &C, hipStream_t st) {
-    if (C.have_last && C.last_stream != st)
-        HIP_TRY(hipStreamWaitEvent(st, C.last_done, 0));
+// Makes `waiter` wait for everything enqueued so far on the previous call's stream.
+int wait_previous(Ctx &C, hipStream_t waiter) {
+    if (!C.have_last || C.last_stream == waiter)
+        return 1;
+    if (hipEventRecord(C.prev_done, C.last_stream) != hipSuccess) {
+        // that stream is gone (destroyed after its call): drain the device instead
+        (void)hipGetLastError();
+        HIP_TRY(hipDeviceSynchronize());
+        C.have_last = false;
+        return 1;
+    }
+    HIP_TRY(hipStreamWaitEvent(waiter, C.prev_done, 0));
     return 1;
 }
 
-int finish_call(Ctx &C, hipStream_t st, PlanSlot *slot) {
-    HIP_TRY(hipEventRecord(slot->done, st));
-    slot->used = true;
-    C.last_done = slot->done;
+int order_after_previous(Ctx &C, hipStream_t st) { return wait_previous(C, st); }
+
+int finish_call(Ctx &C, hipStream_t st, int si) {
+    if (si % Ctx::kGroup == Ctx::kGroup - 1) {
+        const int gi = si / Ctx::kGroup;
+        HIP_TRY(hipEventRecord(C.grp_done[gi], st));
+        C.grp_used[gi] = true;
+        C.open_last = -1;
+    }
     C.last_stream = st;
     C.have_last = true;
     return 1;
@@ -896,12 +923,13 @@ int mvllm_hip_init(int device) {
     HIP_TRY(hipSetDevice(device));
     HIP_TRY(hipStreamCreateWithFlags(&C.own, hipStreamNonBlocking));
     HIP_TRY(hipStreamCreateWithFlags(&C.copy, hipStreamNonBlocking));
-    // Plan-slot events order the host's reuse of a slot and other streams after a call.
-    // Neither needs the call's device writes visible to the host, so they skip the
-    // system-scope release (an L2 write-back between one call's kernels and the next's).
-    for (auto &s : C.slots)
-        HIP_TRY(hipEventCreateWithFlags(&s.done,
-                                        hipEventDisableTiming | hipEventDisableSystemFence));
+    // The plan-slot and ordering events order the host's reuse of a slot and other streams
+    // after a call.  Neither needs the call's device writes visible to the host, so they
+    // skip the system-scope release (an L2 write-back between two calls' kernels).
+    constexpr unsigned kEvFlags = hipEventDisableTiming | hipEventDisableSystemFence;
+    for (auto &e : C.grp_done)
+        HIP_TRY(hipEventCreateWithFlags(&e, kEvFlags));
+    HIP_TRY(hipEventCreateWithFlags(&C.prev_done, kEvFlags));
     C.device = device;
     C.ready = true;
     return 1;
@@ -934,15 +962,20 @@ void mvllm_hip_shutdown(void) {
     for (auto &s : C.slots) {
         s.host.release();
         s.dev.release();
-        (void)hipEventDestroy(s.done);
-        s.done = nullptr;
-        s.used = false;
     }
+    for (int g = 0; g < Ctx::kSlots / Ctx::kGroup; ++g) {
+        (void)hipEventDestroy(C.grp_done[g]);
+        C.grp_done[g] = nullptr;
+        C.grp_used[g] = false;
+    }
+    C.open_last = -1;
+    C.slot_next = 0;
     for (auto &t : C.timed)
         for (auto &e : t.ev)
             (void)hipEventDestroy(e);
     C.timed.clear();
-    C.last_done = nullptr;
+    (void)hipEventDestroy(C.prev_done);
+    C.prev_done = nullptr;
     (void)hipStreamDestroy(C.own);
     (void)hipStreamDestroy(C.copy);
     C.have_last = false;
@@ -1111,8 +1144,8 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
         uint8_t *arena = static_cast<uint8_t *>(C.miss.p);
         size_t off = 0;
         // the arena is reused per call: the copy stream waits for the previous call
-        if (C.have_last)
-            HIP_TRY(hipStreamWaitEvent(C.copy, C.last_done, 0));
+        if (!wait_previous(C, C.copy))
+            return 0;
         for (ExpertWork &w : miss) {
             // the six pieces of an ExpertStore blob are one contiguous host range: one copy
             // (whole-blob DMA runs closer to the PCIe rate than six small ones)
