@@ -32,6 +32,8 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
         lds > kDecLdsBudget)
         return hipErrorInvalidValue;
     a.wgs = a.O / (16 * tiles_wg);
+    if (a.n_cp < 0 || a.n_cp > n_items * a.wgs || (a.n_cp > 0 && !DUAL))
+        return hipErrorInvalidValue;  // every descriptor to copy needs a workgroup
     const dim3 grid((unsigned)(n_items * a.wgs)), block(kDecThreads);
     // staging registers per thread: dual = 8-float chunks of rmax rows, single = uint4 of
     // TERMS planes of rmax rows
@@ -95,9 +97,10 @@ static hipError_t launch_dec_fd(const DecArgs &a, int n_items, int terms, int ks
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
-                           int act, float act_a, float act_b, bool fold, hipStream_t st) {
+                           int act, float act_a, float act_b, bool fold, const DecDesc *cp_src,
+                           DecDesc *cp_dst, int n_cp, hipStream_t st) {
     if (n_items <= 0)
-        return hipSuccess;
+        return n_cp > 0 ? hipErrorInvalidValue : hipSuccess;
     if (K > kDecMaxK)
         return hipErrorInvalidValue;
     DecArgs a{};
@@ -116,6 +119,9 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
     a.act = act;
     a.act_a = act_a;
     a.act_b = act_b;
+    a.cp_src = cp_src;
+    a.cp_dst = cp_dst;
+    a.n_cp = n_cp;
     if (fmt == 4)
         return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st)
                     : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st);

@@ -62,6 +62,12 @@ struct DecArgs {
     float *hp;            // dual, fmt 4: H partial sums [O/64][4][rcap]
     float *out;           // single: Y [rcap][O] f32, or the caller's out [S][O] with fold
     int fold;             // single: add wts[r] * y into out[rows[r]] (float atomics)
+    // dual: workgroups [0, n_cp) copy descriptor i of cp_src (the down launch's, in host
+    // memory) to cp_dst (device memory): the down kernel then starts from an HBM/L2 read
+    // instead of a PCIe round trip (measured 20.6 -> 18.4 us at c1 T=16)
+    const DecDesc *cp_src;
+    DecDesc *cp_dst;
+    int n_cp;
     int wgs;              // workgroups per item
     int K, O, rcap, rmax;
     int act;
@@ -318,6 +324,16 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     static_assert(!DUAL || NT == 2, "dual waves carry a gate and an up tile");
     item = __builtin_amdgcn_readfirstlane(item);
     wg = __builtin_amdgcn_readfirstlane(wg);
+    // the down descriptor this workgroup copies (wave 0): 16 bytes a lane, lanes l and
+    // l + 16 k reading the same bytes (four requests; one 4-byte request a lane slowed
+    // every workgroup's descriptor read over PCIe).  Issued first, stored with the staging
+    // below: vector loads complete in order, so nothing waits for it early.
+    const int cpi = item * A.wgs + wg;
+    const bool cp =
+        DUAL && !FUSED && cpi < A.n_cp && __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
+    u32x4 cpv = {0u, 0u, 0u, 0u};
+    if (cp)
+        cpv = reinterpret_cast<const u32x4 *>(A.cp_src + cpi)[tid & 15];
     const DecDesc &dd = A.desc[item];
     const int K = A.K, O = A.O;
     const int nrow = dd.nrow, jbase = dd.jbase;
@@ -533,6 +549,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
         if (tid < 32)
             lcomb[tid] = comb;
     }
+    if (cp)
+        reinterpret_cast<u32x4 *>(A.cp_dst + cpi)[tid & 15] = cpv;
     __syncthreads();
 
     // 4) MFMA over this wave's K blocks with NU in flight: b[u] holds block k0 + u; the

@@ -487,6 +487,7 @@ struct DevPlan {
     int *xrow, *tok_ptr, *ent_row, *out_row, *items, *rdest;
     float *ent_w, *rw;
     DecDesc *gu_desc, *dn_desc;  // decode kernels: one descriptor per item of each phase
+    DecDesc *dn_desc_dev;        // dn_desc in device memory (a copy the gate/up kernel makes)
     int slot;  // plan slot index
 };
 
@@ -623,6 +624,9 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.rw = reinterpret_cast<float *>(d + o_rw);
     dp.gu_desc = reinterpret_cast<DecDesc *>(d + o_dg);
     dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
+    dp.dn_desc_dev = reinterpret_cast<DecDesc *>(static_cast<char *>(s.dev.p) + o_dd);
+    if (!zero_copy)
+        dp.dn_desc_dev = dp.dn_desc;  // already there
     dp.slot = si;
     return 1;
 }
@@ -771,6 +775,11 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
         const size_t tb = (size_t)cc.terms * 2;
         HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
         HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
+        // the gate/up workgroups copy the down descriptors from the pinned plan slot to
+        // device memory (when they are not there already), a descriptor a workgroup
+        const int n_dn = static_cast<int>(cc.dn.it1 - cc.dn.it0);
+        const int wgs_gu = I / (16 * (kDecWaves / cc.gu.ks));
+        int copied = dp.dn_desc_dev == dp.dn_desc ? n_dn : 0;
         for (int part = 0; part < 2; ++part) {
             const size_t i0 = part ? cc.gu.it_split : cc.gu.it0;
             const size_t i1 = part ? cc.gu.it1 : cc.gu.it_split;
@@ -778,19 +787,27 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
             if (i1 <= i0)
                 continue;
+            const int ncp = std::min(n_dn - copied, static_cast<int>(i1 - i0) * wgs_gu);
             HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.nt,
                                     dp.gu_desc + (i0 - cc.gu.it0), static_cast<int>(i1 - i0), in,
                                     nullptr, nullptr, C.Ph.p, static_cast<float *>(C.HP.p),
-                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, false, st));
+                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, false,
+                                    dp.dn_desc + copied, dp.dn_desc_dev + copied, ncp, st));
+            copied += ncp;
             C.stats[13] += 1;
         }
+        if (copied < n_dn)  // more down items than gate/up workgroups
+            HIP_TRY(hipMemcpyAsync(dp.dn_desc_dev + copied, dp.dn_desc + copied,
+                                   (size_t)(n_dn - copied) * sizeof(DecDesc),
+                                   hipMemcpyHostToDevice, st));
         if (C.timing)
             HIP_TRY(hipEventRecord(tc.ev[1], st));
-        HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.nt, dp.dn_desc,
+        HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.nt, dp.dn_desc_dev,
                                 static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, C.Ph.p,
                                 static_cast<const float *>(C.HP.p), nullptr, nullptr,
                                 cc.atomic_combine ? out : static_cast<float *>(C.Y.p), I, D,
-                                rcap, cc.dn.rmax, 0, 0.f, 0.f, cc.atomic_combine, st));
+                                rcap, cc.dn.rmax, 0, 0.f, 0.f, cc.atomic_combine, nullptr,
+                                nullptr, 0, st));
         C.stats[14] += 1;
     } else {
         for (int part = 0; part < 2; ++part) {
