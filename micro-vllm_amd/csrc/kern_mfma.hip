@@ -9,13 +9,13 @@
 namespace mvllm_hip {
 
 
-template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR>
+template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool PACK>
 __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void k_mfma_dec(DecArgs A) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int item = blockIdx.x / A.wgs;
-    dec_task<FMT, DUAL, TERMS, KS, NT, SR, false>(A, item, blockIdx.x - item * A.wgs,
-                                                  (int)threadIdx.x, smem, DecSync{});
+    dec_task<FMT, DUAL, TERMS, KS, NT, SR, false, PACK>(A, item, blockIdx.x - item * A.wgs,
+                                                        (int)threadIdx.x, smem, DecSync{});
 }
 
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt) {
@@ -47,12 +47,24 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
         return e;
     };
     hipError_t e;
-    if (DUAL ? sr <= 2 : sr <= 4)
-        e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, DUAL ? 2 : 4>);
-    else if (DUAL ? sr <= kDecStageDual : sr <= kDecStageSingle)
-        e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, DUAL ? kDecStageDual : kDecStageSingle>);
-    else
+    constexpr int SR1 = DUAL ? 2 : 4, SR2 = DUAL ? kDecStageDual : kDecStageSingle;
+    if (a.pack && (TERMS != 2 || a.rmax > 8))
         return hipErrorInvalidValue;
+    if (DUAL ? sr <= 2 : sr <= 4) {
+        if constexpr (TERMS == 2)
+            e = a.pack ? go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, true>)
+                       : go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>);
+        else
+            e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>);
+    } else if (DUAL ? sr <= kDecStageDual : sr <= kDecStageSingle) {
+        if constexpr (TERMS == 2)
+            e = a.pack ? go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, true>)
+                       : go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>);
+        else
+            e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>);
+    } else {
+        return hipErrorInvalidValue;
+    }
     if (e != hipSuccess)
         return e;
     return hipGetLastError();
@@ -97,8 +109,8 @@ static hipError_t launch_dec_fd(const DecArgs &a, int n_items, int terms, int ks
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
-                           int act, float act_a, float act_b, bool fold, const DecDesc *cp_src,
-                           DecDesc *cp_dst, int n_cp, hipStream_t st) {
+                           int act, float act_a, float act_b, bool fold, bool pack,
+                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st) {
     if (n_items <= 0)
         return n_cp > 0 ? hipErrorInvalidValue : hipSuccess;
     if (K > kDecMaxK)
@@ -122,6 +134,7 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
     a.cp_src = cp_src;
     a.cp_dst = cp_dst;
     a.n_cp = n_cp;
+    a.pack = pack ? 1 : 0;
     if (fmt == 4)
         return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st)
                     : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st);

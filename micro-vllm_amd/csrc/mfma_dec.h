@@ -68,6 +68,7 @@ struct DecArgs {
     const DecDesc *cp_src;
     DecDesc *cp_dst;
     int n_cp;
+    int pack;  // every item has <= 8 rows and TERMS == 2: the packed kernel is launched
     int wgs;              // workgroups per item
     int K, O, rcap, rmax;
     int act;
@@ -122,8 +123,11 @@ __device__ __forceinline__ void load_scales(u32x4 (&sc)[2], __amdgpu_buffer_rsrc
 // EXACT is the redo of a wave's tiles whose operands the common path does not reproduce
 // (see dec_needs_exact): it decodes per element, MXFP4 through decode_b7_exact, int4 as
 // n - 8 with chains from 0 and a non-finite scale inside each product.
-template <int FMT, int TERMS, int NT, bool EXACT>
-__device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS][2],
+// PACK (two terms, items of <= 8 rows): A row t holds term t / 8 of row t % 8, so one
+// MFMA takes both terms (tb already points at this lane's term) and C rows r and r + 8
+// are added after the loop: half the matrix-core work and A reads per block.
+template <int FMT, int TERMS, int NT, bool EXACT, bool PACK = false>
+__device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[PACK ? 1 : TERMS][2],
                                                const DBlock<FMT> (&b)[NT],
                                                const u32x4 (&sc)[NT][2], int kl, const char *tb,
                                                int t, int nrow, const float *lxs, int kb, int q,
@@ -139,9 +143,9 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
         // region per group instead of merging them (register pressure).
         int nr = nrow;
         asm volatile("" : "+v"(nr));
-        if (t < nr) {
+        if ((PACK ? (t & 7) : t) < nr) {
 #pragma unroll
-            for (int tm = 0; tm < TERMS; ++tm)
+            for (int tm = 0; tm < (PACK ? 1 : TERMS); ++tm)
 #pragma unroll
                 for (int s = 0; s < 2; ++s)
                     a[tm][s] = *reinterpret_cast<const bf16x8 *>(
@@ -202,7 +206,7 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
                 // scale per (row, group) then applies
                 f4v c = c0;
 #pragma unroll
-                for (int tm = 0; tm < TERMS; ++tm) {
+                for (int tm = 0; tm < (PACK ? 1 : TERMS); ++tm) {
                     bf16x8 b0 = B0, b1 = B1;
                     if (EXACT && tm > 0 && spec)
                         b0 = b1 = bf16x8{};
@@ -217,7 +221,7 @@ __device__ __forceinline__ void compute_dblock(f4v (&acc)[NT], bf16x8 (&a)[TERMS
                 asm volatile("" : "+v"(acc[n]));
             } else {
 #pragma unroll
-                for (int tm = 0; tm < TERMS; ++tm) {
+                for (int tm = 0; tm < (PACK ? 1 : TERMS); ++tm) {
                     acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], B0, acc[n], 0, 0, 0);
                     acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], B1, acc[n], 0, 0, 0);
                 }
@@ -315,7 +319,7 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
 }
 
 // One task: item `item`, column block `wg` of one projection.  FUSED adds the hooks.
-template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool FUSED>
+template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool FUSED, bool PACK = false>
 __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int tid,
                                          char *smem, const DecSync &sy) {
     constexpr int TW = kDecWaves / KS;   // wave slots per K range
@@ -559,19 +563,22 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
 #pragma unroll
     for (int n = 0; n < NT; ++n)
         acc[n] = f4v{0.f, 0.f, 0.f, 0.f};
-    const char *ta = reinterpret_cast<const char *>(lp) + (size_t)(t < nrow ? t : 0) * rsb +
-                     (size_t)(2 * q) * TERMS * 16;
+    static_assert(!PACK || TERMS == 2, "packing puts two terms into one MFMA");
+    // this lane's A row (PACK: row t % 8, term t / 8)
+    const int ar = PACK ? (t & 7) : t;
+    const char *ta = reinterpret_cast<const char *>(lp) + (size_t)(ar < nrow ? ar : 0) * rsb +
+                     (size_t)(2 * q) * TERMS * 16 + (PACK ? (t >> 3) * 16 : 0);
     const int src4 = 4 * (4 * t + q);  // ds_bpermute byte address of lane 4 t + q
-    bf16x8 a[TERMS][2] = {};           // A fragments; stay zero in rows t >= nrow
+    bf16x8 a[PACK ? 1 : TERMS][2] = {};  // A fragments; stay zero in rows past nrow
     // checked before the loop, while its first weight loads are in flight (the first
     // block needs the scales anyway); at the end it would lengthen every wave's tail
     const bool exc = __builtin_amdgcn_ballot_w64(
                          dec_needs_exact<FMT>(sc, q, nblk, lxs + (kw0 >> 6) * 16, lane)) != 0;
     auto consume = [&](const DBlock<FMT>(&bb)[NT], int kl) {
         const int kb = kw0 + 256 * kl;
-        compute_dblock<FMT, TERMS, NT, false>(acc, a, bb, sc, kl,
-                                              ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow, lxs,
-                                              kb, q, src4);
+        compute_dblock<FMT, TERMS, NT, false, PACK>(acc, a, bb, sc, kl,
+                                                    ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow,
+                                                    lxs, kb, q, src4);
     };
     auto reload = [&](DBlock<FMT>(&bb)[NT], int kl) {
 #pragma unroll
@@ -598,6 +605,13 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     for (int u = 0; u < NU; ++u)
         if (k0 + NU + u < nblk)
             consume(b[u], k0 + NU + u);
+    if constexpr (PACK) {  // C row r + 8 holds the low term's part of row r
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                acc[n][i] += __shfl_xor(acc[n][i], 32);
+    }
     {
         // Rare: operands the common path does not reproduce in this wave's tiles.  Redo
         // the tiles block by block with the exact decode; the streaming loop above then
@@ -606,13 +620,17 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
 #pragma unroll
             for (int n = 0; n < NT; ++n)
                 acc[n] = f4v{0.f, 0.f, 0.f, 0.f};
+            // unpacked: the exact int4 path keeps the low terms out of non-finite products
+            const char *tu = reinterpret_cast<const char *>(lp) +
+                             (size_t)(t < nrow ? t : 0) * rsb + (size_t)(2 * q) * TERMS * 16;
+            bf16x8 au[TERMS][2] = {};
 #pragma unroll 1
             for (int kl = 0; kl < nblk; ++kl) {
                 DBlock<FMT> bb[NT];
                 reload(bb, kl);
                 const int kb = kw0 + 256 * kl;
-                compute_dblock<FMT, TERMS, NT, true>(acc, a, bb, sc, kl,
-                                                     ta + (size_t)(kb >> 3) * TERMS * 16, t, nrow,
+                compute_dblock<FMT, TERMS, NT, true>(acc, au, bb, sc, kl,
+                                                     tu + (size_t)(kb >> 3) * TERMS * 16, t, nrow,
                                                      lxs, kb, q, src4);
             }
         }

@@ -102,8 +102,8 @@ size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks,
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
-                           int act, float act_a, float act_b, bool fold, const DecDesc *cp_src,
-                           DecDesc *cp_dst, int n_cp, hipStream_t st);
+                           int act, float act_a, float act_b, bool fold, bool pack,
+                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st);
 
 // Both decode projections in one cooperative launch (kern_fused.hip), the down projection
 // folding the combine into out.  Descriptors as for launch_mfma_dec, plus: pad0[0] =

@@ -779,6 +779,17 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
         // device memory (when they are not there already), a descriptor a workgroup
         const int n_dn = static_cast<int>(cc.dn.it1 - cc.dn.it0);
         const int wgs_gu = I / (16 * (kDecWaves / cc.gu.ks));
+        // Items of <= 8 rows with two terms: the packed kernels (both terms in one MFMA),
+        // launched with that row capacity.
+        auto max_rows = [&](size_t i0, size_t i1) {
+            int m = 1;
+            for (size_t i = i0; i < i1; ++i)
+                m = std::max(m, cc.items[4 * i + 2]);
+            return m;
+        };
+        const int mr_gu = max_rows(cc.gu.it0, cc.gu.it1), mr_dn = max_rows(cc.dn.it0, cc.dn.it1);
+        const bool pk_gu = cc.terms == 2 && mr_gu <= 8, pk_dn = cc.terms == 2 && mr_dn <= 8;
+        const int rmax_gu = pk_gu ? mr_gu : cc.gu.rmax, rmax_dn = pk_dn ? mr_dn : cc.dn.rmax;
         int copied = dp.dn_desc_dev == dp.dn_desc ? n_dn : 0;
         for (int part = 0; part < 2; ++part) {
             const size_t i0 = part ? cc.gu.it_split : cc.gu.it0;
@@ -791,7 +802,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.nt,
                                     dp.gu_desc + (i0 - cc.gu.it0), static_cast<int>(i1 - i0), in,
                                     nullptr, nullptr, C.Ph.p, static_cast<float *>(C.HP.p),
-                                    nullptr, D, I, rcap, cc.gu.rmax, act, a, b, false,
+                                    nullptr, D, I, rcap, rmax_gu, act, a, b, false, pk_gu,
                                     dp.dn_desc + copied, dp.dn_desc_dev + copied, ncp, st));
             copied += ncp;
             C.stats[13] += 1;
@@ -806,7 +817,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                                 static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, C.Ph.p,
                                 static_cast<const float *>(C.HP.p), nullptr, nullptr,
                                 cc.atomic_combine ? out : static_cast<float *>(C.Y.p), I, D,
-                                rcap, cc.dn.rmax, 0, 0.f, 0.f, cc.atomic_combine, nullptr,
+                                rcap, rmax_dn, 0, 0.f, 0.f, cc.atomic_combine, pk_dn, nullptr,
                                 nullptr, 0, st));
         C.stats[14] += 1;
     } else {
