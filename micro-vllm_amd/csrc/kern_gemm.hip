@@ -4,19 +4,22 @@
 // Work item = (expert, block of up to 16 * MT of its rows) x (block of output columns).
 // A workgroup of 8 waves streams K in steps of 256:
 //   * activations (A): the item's rows of the bf16 input planes [TERMS][rcap][K] are
-//     staged into LDS, double buffered, by all 512 threads (16-byte loads); for int4
-//     the per-64 sums of each row (the -8 offset correction) come along;
+//     staged into LDS, double buffered, by all 512 threads (16-byte loads);
 //   * weights (B): each wave owns two 16-column tiles (gate and up at the same columns
 //     for the dual projection, two adjacent tiles of the down matrix otherwise) and
 //     reads their packed rows with coalesced 8-byte loads (lane l -> row l / 4, 32 B
 //     per row per load) two steps ahead, moves them into the operand layout with
-//     ds_bpermute and decodes them exactly in registers, as the decode kernel does;
+//     ds_bpermute and decodes them exactly in registers; the tiles' scales come once per
+//     pair of steps and are handed out the same way;
 //   * each decoded B fragment feeds MT row tiles (one A fragment read per two MFMAs).
-// int4: every 64-wide group is its own chain started from -8 * (group sum of the row),
-// then one f32 FMA applies the group's f32 scale (exact (n - 8) * scale, no rounding of
-// the product to bf16).  MXFP4: the ue8m0 scale is folded into the bf16 decode (exact).
-// The dual epilogue applies the activation and writes H in the same plane format (with
-// per-16-column partial sums for int4) that both down kernels read.
+// int4: nibble n decodes to bf16(n - 8) exactly (signed e4m3 codes through the
+// converter), every 64-wide group is its own chain from 0, and one f32 FMA applies the
+// group's f32 scale (exact (n - 8) * scale, no rounding of the product to bf16).
+// MXFP4: the ue8m0 scale is folded into the bf16 decode (exact for bytes 2..252).  Other
+// operands (MXFP4 bytes outside that range, non-finite int4 scales) send the task
+// through a second pass with the per-element exact decode.
+// The dual epilogue applies the activation and writes H in the same plane format that
+// the down kernel reads.
 #include "mfma_common.h"
 
 #include <algorithm>
