@@ -517,12 +517,10 @@ static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int 
         case 1: return launch_gemm_t<FMT, DUAL, 1, 1>(a, n_items, st);
         case 2: return launch_gemm_t<FMT, DUAL, 1, 2>(a, n_items, st);
         }
-        if constexpr (FMT == 7) {
-            if (mt == 4)
-                return launch_gemm_t<FMT, DUAL, 1, 4>(a, n_items, st);
-            if (mt == 8)
-                return launch_gemm_t<FMT, DUAL, 1, 8>(a, n_items, st);
-        }
+        if (mt == 4)
+            return launch_gemm_t<FMT, DUAL, 1, 4>(a, n_items, st);
+        if (mt == 8)
+            return launch_gemm_t<FMT, DUAL, 1, 8>(a, n_items, st);
         return hipErrorInvalidValue;
     }
     if (terms == 2) {
@@ -530,10 +528,8 @@ static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int 
         case 1: return launch_gemm_t<FMT, DUAL, 2, 1>(a, n_items, st);
         case 2: return launch_gemm_t<FMT, DUAL, 2, 2>(a, n_items, st);
         }
-        if constexpr (FMT == 7) {
-            if (mt == 4)
-                return launch_gemm_t<FMT, DUAL, 2, 4>(a, n_items, st);
-        }
+        if (mt == 4)
+            return launch_gemm_t<FMT, DUAL, 2, 4>(a, n_items, st);
         return hipErrorInvalidValue;
     }
     return hipErrorInvalidValue;

@@ -129,9 +129,10 @@ hipError_t launch_mfma_fused(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn
 // 16-byte (int4) / 8-byte (MXFP4) aligned scales and 16-byte aligned planes.  Inputs are
 // bf16 planes [terms][rcap][K] (int4: K in the 8-block slot order of the decode
 // kernel); launch_prep_planes builds them from f32 rows.
-// Largest row-tile count per workgroup that compiles without spills: int4 carries a
-// per-group chain and scale per row tile, so it stops at 2 tiles (32 rows).
-inline int gemm_max_mt(int fmt, int terms) { return fmt == 4 ? 2 : terms == 1 ? 8 : 4; }
+// Largest row-tile count per workgroup: 8 (128 rows) with one term, 4 with two, for both
+// formats (int4 decodes n - 8 directly and needs no per-row sums).  Larger blocks read an
+// expert's weights fewer times; MT = 8 spills at most 5 registers.
+inline int gemm_max_mt(int fmt, int terms) { return (void)fmt, terms == 1 ? 8 : 4; }
 size_t gemm_lds_bytes(int fmt, int terms, int mt);
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,
