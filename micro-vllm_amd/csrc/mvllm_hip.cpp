@@ -349,11 +349,12 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
     size_t n_items = 0;
     for (const ExpertWork &w : P.ew)
         n_items += (size_t)((w.nrows + ph.rmax - 1) / ph.rmax);
-    // Two workgroups of kDecWaves waves share a CU.  Each wave streams nt tiles x K/ks;
-    // pick the admissible (ks, nt) minimising rounds x per-wave blocks (+ a fixed ramp of
-    // ~4 blocks per round) over the 256 CUs.
+    // Each wave streams nt tiles x K/ks.  Cost of an admissible (ks, nt): the busiest of
+    // the 256 CUs runs n = ceil(workgroups / 256) workgroups, each its waves' blocks plus a
+    // ramp of ~4 blocks; two workgroups sharing a CU overlap by ~15 %.  Ties keep the
+    // smaller split.  This picks the fastest choice measured on MI355X at c1 T = 1, 2, 4, 8
+    // and 16 and at c2, for both projections.
     const size_t tiles = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // 16-row weight tiles
-    const size_t slots = 256 * (size_t)(2 * 8 / kDecWaves);           // resident workgroups
     double best = 1e30;
     for (const auto &kt : kDecOpts[dual ? 1 : 0]) {
         if (!kt[0] || !dec_fits(fmt, K, O, ph.rmax, cc.terms, dual, kt[0], kt[1]))
@@ -361,8 +362,9 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
         if (C.dec_ks && kt[0] != C.dec_ks)
             continue;
         const size_t wgs = tiles * (size_t)kt[0] / ((size_t)kDecWaves * (size_t)kt[1]);
-        const double rounds = (double)((wgs + slots - 1) / slots);
-        const double cost = rounds * ((double)(K / 256) * kt[1] / kt[0] + 4.0);
+        const double per_cu = (double)((wgs + 255) / 256);
+        const double cost = per_cu * ((double)(K / 256) * kt[1] / kt[0] + 4.0) /
+                            (per_cu >= 2 ? 1.15 : 1.0);
         if (cost < best - 1e-9) {
             best = cost;
             ph.ks = kt[0];

@@ -184,6 +184,27 @@ def test_moe_block_dev_parity(hip, orc, case):
     assert err < TOL_F32
 
 
+@pytest.mark.parametrize("ci,ks", [(1, 1), (1, 2), (1, 4), (7, 2), (7, 4), (-2, 1), (-2, 2),
+                                   (-2, 4)])
+def test_decode_k_split_parity(hip, orc, ci, ks):
+    """Every K split of the decode kernels that both projections admit (option dec_ks),
+    including those the planner does not pick for these shapes."""
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case = DEV_CASES[ci]
+    say("dec_ks", ks, case)
+    rng = np.random.default_rng(D * 41 + I + ks)
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    hip.stats_reset()
+    assert hip.set_option("dec_ks", ks)
+    try:
+        got = run_dev(hip, c, act, a, b)
+    finally:
+        hip.set_option("dec_ks", 0)
+    exp = oracle_out(orc, c, act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err, hip.stats())
+    assert err < TOL_F32
+
+
 @pytest.mark.parametrize("case", DEV_CASES[::2])
 def test_moe_block_host_parity(hip, orc, case):
     fmt, D, I, nr, S, act, a, b, nulls, bad = case
