@@ -435,32 +435,48 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
 
 // ---- input planes for the GEMM: gather, split into bf16 terms ------------------------
 
-// One thread per 8-element chunk of a row.
+// One workgroup per row j of the planes: the source row is one scalar load, and each
+// thread converts up to 4 of the row's 8-element chunks per pass with all their loads
+// issued first (clamped to the row, so they stay unconditional; only the stores are).
+constexpr int kPrepThreads = 256, kPrepUnroll = 4;
+
 template <int FMT, int TERMS>
-__global__ __launch_bounds__(256) void k_prep_planes(const float *x, const int *rows_map, int R,
-                                                     int K, int rcap, __bf16 *planes) {
+__global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
+                                                              const int *rows_map, int K,
+                                                              int rcap, __bf16 *planes) {
+    const int j = blockIdx.x;
+    const int src = rows_map ? rows_map[j] : j;
     const int per_row = K >> 3;
-    const size_t total = (size_t)R * per_row;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += stride) {
-        const int j = (int)(idx / per_row);
-        const int c = (int)(idx - (size_t)j * per_row);
-        const int src = rows_map ? rows_map[j] : j;
-        const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)src * K + 8 * c);
-        const float4 v0 = p[0], v1 = p[1];
-        const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-        bf16x8 o[3];
+    const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)src * K);
+    for (int c0 = 0; c0 < per_row; c0 += kPrepUnroll * kPrepThreads) {
+        float4 v[kPrepUnroll][2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            __bf16 tt[3];
-            split_terms<TERMS>(v[e], tt);
-#pragma unroll
-            for (int tm = 0; tm < TERMS; ++tm)
-                o[tm][a_slot<FMT>(e)] = tt[tm];
+        for (int u = 0; u < kPrepUnroll; ++u) {
+            const int c = min(c0 + u * kPrepThreads + (int)threadIdx.x, per_row - 1);
+            v[u][0] = p[2 * c];
+            v[u][1] = p[2 * c + 1];
         }
 #pragma unroll
-        for (int tm = 0; tm < TERMS; ++tm)
-            *reinterpret_cast<bf16x8 *>(planes + ((size_t)tm * rcap + j) * K + 8 * c) = o[tm];
+        for (int u = 0; u < kPrepUnroll; ++u) {
+            const int c = c0 + u * kPrepThreads + (int)threadIdx.x;
+            const float e8[8] = {v[u][0].x, v[u][0].y, v[u][0].z, v[u][0].w,
+                                 v[u][1].x, v[u][1].y, v[u][1].z, v[u][1].w};
+            bf16x8 o[3];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                __bf16 tt[3];
+                split_terms<TERMS>(e8[e], tt);
+#pragma unroll
+                for (int tm = 0; tm < TERMS; ++tm)
+                    o[tm][a_slot<FMT>(e)] = tt[tm];
+            }
+            if (c < per_row) {
+#pragma unroll
+                for (int tm = 0; tm < TERMS; ++tm)
+                    *reinterpret_cast<bf16x8 *>(planes + ((size_t)tm * rcap + j) * K + 8 * c) =
+                        o[tm];
+            }
+        }
     }
 }
 
@@ -571,12 +587,10 @@ hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *row
         return hipSuccess;
     if (K % 8)
         return hipErrorInvalidValue;
-    const size_t total = (size_t)R * (K / 8);
-    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
     __bf16 *pl = static_cast<__bf16 *>(planes);
 #define MVLLM_PREP(F, T)                                                                      \
-    hipLaunchKernelGGL((k_prep_planes<F, T>), dim3(blocks), dim3(256), 0, st, x, rows_map, R, \
-                       K, rcap, pl)
+    hipLaunchKernelGGL((k_prep_planes<F, T>), dim3((unsigned)R), dim3(kPrepThreads), 0, st, x, \
+                       rows_map, K, rcap, pl)
     if (fmt == 4) {
         if (terms == 1) MVLLM_PREP(4, 1); else if (terms == 2) MVLLM_PREP(4, 2); else MVLLM_PREP(4, 3);
     } else if (fmt == 7) {
