@@ -99,6 +99,9 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
  *            kernel with float atomics (same products, any summation order).
  *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
  *   "dec_ks" 0 = automatic; 1, 2, 4 or 8 forces the split of K across waves.
+ *   "dec_inline" 1 (default) = the decode gate/up launch carries its descriptors in
+ *            its kernel arguments (at most 64 items; same results); 0 = it reads them
+ *            from the pinned plan slot.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
  *   "fuse"   1 = decode calls with every expert resident run both projections in one
  *            cooperative launch: the down tasks stream their weights while the gate/up

@@ -5,6 +5,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 namespace mvllm_hip {
 
@@ -18,13 +19,23 @@ void k_mfma_dec(DecArgs A) {
                                                         (int)threadIdx.x, smem, DecSync{});
 }
 
+// Gate/up with its descriptors in the kernel arguments (device memory at launch).
+template <int FMT, int TERMS, int KS, int SR, bool PACK>
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void k_mfma_dec_inl(DecArgs A, DecInline I) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int item = blockIdx.x / A.wgs;
+    dec_task<FMT, true, TERMS, KS, 2, SR, false, PACK, true>(
+        A, item, blockIdx.x - item * A.wgs, (int)threadIdx.x, smem, DecSync{}, I.d);
+}
+
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt) {
     (void)dual;
     return dec_lds_plan(fmt, K, rmax, terms, ks, nt, nullptr);
 }
 
 template <int FMT, bool DUAL, int TERMS, int KS, int NT>
-static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
+static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const DecDescK *inl) {
     const size_t lds = mfma_dec_lds_bytes(FMT, a.K, a.rmax, TERMS, DUAL, KS, NT);
     const int tiles_wg = (kDecWaves / KS) * (DUAL ? 1 : NT);  // column tiles per workgroup
     if (a.K % 512 || a.K % (256 * KS) || a.K / KS > dec_max_kr(FMT) || a.O % (16 * tiles_wg) ||
@@ -39,29 +50,57 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
     // TERMS planes of rmax rows
     const size_t need = DUAL ? (size_t)a.rmax * (a.K / 8) : (size_t)TERMS * a.rmax * (a.K / 8);
     const int sr = (int)((need + kDecThreads - 1) / kDecThreads);
-    auto go = [&](auto kern) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e == hipSuccess)
-            hipLaunchKernelGGL(kern, grid, block, lds, st, a);
+    if (inl && (!DUAL || n_items > kDecInline))
+        return hipErrorInvalidValue;
+    DecInline di;
+    if (inl)
+        std::copy(inl, inl + n_items, di.d);
+    auto go = [&](auto kern, auto kern_inl, auto has_inl) {
+        constexpr bool HI = decltype(has_inl)::value;
+        const void *f = HI && inl ? reinterpret_cast<const void *>(kern_inl)
+                                  : reinterpret_cast<const void *>(kern);
+        hipError_t e =
+            hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess)
+            return e;
+        if constexpr (HI) {
+            if (inl) {
+                hipLaunchKernelGGL(kern_inl, grid, block, lds, st, a, di);
+                return e;
+            }
+        }
+        hipLaunchKernelGGL(kern, grid, block, lds, st, a);
         return e;
+    };
+    // the compact-descriptor kernel of the same configuration (gate/up only)
+    auto with_inl = [&](auto kern, auto sr_c, auto pack_c) {
+        constexpr int SRv = decltype(sr_c)::value;
+        constexpr bool PKv = decltype(pack_c)::value;
+        if constexpr (DUAL && NT == 2)
+            return go(kern, k_mfma_dec_inl<FMT, TERMS, KS, SRv, PKv>, std::true_type{});
+        else
+            return go(kern, kern, std::false_type{});
     };
     hipError_t e;
     constexpr int SR1 = DUAL ? 2 : 4, SR2 = DUAL ? kDecStageDual : kDecStageSingle;
+    using S1 = std::integral_constant<int, SR1>;
+    using S2 = std::integral_constant<int, SR2>;
+    using PT = std::true_type;
+    using PF = std::false_type;
     if (a.pack && (TERMS != 2 || a.rmax > 8))
         return hipErrorInvalidValue;
     if (DUAL ? sr <= 2 : sr <= 4) {
         if constexpr (TERMS == 2)
-            e = a.pack ? go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, true>)
-                       : go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>);
+            e = a.pack ? with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, true>, S1{}, PT{})
+                       : with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>, S1{}, PF{});
         else
-            e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>);
+            e = with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR1, false>, S1{}, PF{});
     } else if (DUAL ? sr <= kDecStageDual : sr <= kDecStageSingle) {
         if constexpr (TERMS == 2)
-            e = a.pack ? go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, true>)
-                       : go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>);
+            e = a.pack ? with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, true>, S2{}, PT{})
+                       : with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>, S2{}, PF{});
         else
-            e = go(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>);
+            e = with_inl(k_mfma_dec<FMT, DUAL, TERMS, KS, NT, SR2, false>, S2{}, PF{});
     } else {
         return hipErrorInvalidValue;
     }
@@ -71,26 +110,27 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st) {
 }
 
 template <int FMT, bool DUAL, int TERMS>
-static hipError_t launch_dec_k(const DecArgs &a, int n_items, int ks, int nt, hipStream_t st) {
+static hipError_t launch_dec_k(const DecArgs &a, int n_items, int ks, int nt, hipStream_t st,
+                               const DecDescK *inl) {
     if constexpr (DUAL) {
         if (nt != 2)
             return hipErrorInvalidValue;
         switch (ks) {
-        case 1: return launch_dec_t<FMT, true, TERMS, 1, 2>(a, n_items, st);
-        case 2: return launch_dec_t<FMT, true, TERMS, 2, 2>(a, n_items, st);
-        case 4: return launch_dec_t<FMT, true, TERMS, 4, 2>(a, n_items, st);
-        case 8: return launch_dec_t<FMT, true, TERMS, 8, 2>(a, n_items, st);
+        case 1: return launch_dec_t<FMT, true, TERMS, 1, 2>(a, n_items, st, inl);
+        case 2: return launch_dec_t<FMT, true, TERMS, 2, 2>(a, n_items, st, inl);
+        case 4: return launch_dec_t<FMT, true, TERMS, 4, 2>(a, n_items, st, inl);
+        case 8: return launch_dec_t<FMT, true, TERMS, 8, 2>(a, n_items, st, inl);
         default: return hipErrorInvalidValue;
         }
     } else {
         if (nt == 2)
-            return ks == 1 ? launch_dec_t<FMT, false, TERMS, 1, 2>(a, n_items, st)
+            return ks == 1 ? launch_dec_t<FMT, false, TERMS, 1, 2>(a, n_items, st, inl)
                            : hipErrorInvalidValue;
         switch (ks) {
-        case 1: return launch_dec_t<FMT, false, TERMS, 1, 1>(a, n_items, st);
-        case 2: return launch_dec_t<FMT, false, TERMS, 2, 1>(a, n_items, st);
-        case 4: return launch_dec_t<FMT, false, TERMS, 4, 1>(a, n_items, st);
-        case 8: return launch_dec_t<FMT, false, TERMS, 8, 1>(a, n_items, st);
+        case 1: return launch_dec_t<FMT, false, TERMS, 1, 1>(a, n_items, st, inl);
+        case 2: return launch_dec_t<FMT, false, TERMS, 2, 1>(a, n_items, st, inl);
+        case 4: return launch_dec_t<FMT, false, TERMS, 4, 1>(a, n_items, st, inl);
+        case 8: return launch_dec_t<FMT, false, TERMS, 8, 1>(a, n_items, st, inl);
         default: return hipErrorInvalidValue;
         }
     }
@@ -98,19 +138,20 @@ static hipError_t launch_dec_k(const DecArgs &a, int n_items, int ks, int nt, hi
 
 template <int FMT, bool DUAL>
 static hipError_t launch_dec_fd(const DecArgs &a, int n_items, int terms, int ks, int nt,
-                                hipStream_t st) {
+                                hipStream_t st, const DecDescK *inl) {
     if (terms <= 1)
-        return launch_dec_k<FMT, DUAL, 1>(a, n_items, ks, nt, st);
+        return launch_dec_k<FMT, DUAL, 1>(a, n_items, ks, nt, st, inl);
     if (terms == 2)
-        return launch_dec_k<FMT, DUAL, 2>(a, n_items, ks, nt, st);
-    return launch_dec_k<FMT, DUAL, 3>(a, n_items, ks, nt, st);
+        return launch_dec_k<FMT, DUAL, 2>(a, n_items, ks, nt, st, inl);
+    return launch_dec_k<FMT, DUAL, 3>(a, n_items, ks, nt, st, inl);
 }
 
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
-                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st) {
+                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
+                           const DecDescK *inl) {
     if (n_items <= 0)
         return n_cp > 0 ? hipErrorInvalidValue : hipSuccess;
     if (K > kDecMaxK)
@@ -136,11 +177,11 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
     a.n_cp = n_cp;
     a.pack = pack ? 1 : 0;
     if (fmt == 4)
-        return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st)
-                    : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st);
+        return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st, inl)
+                    : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st, inl);
     if (fmt == 7)
-        return dual ? launch_dec_fd<7, true>(a, n_items, terms, ks, nt, st)
-                    : launch_dec_fd<7, false>(a, n_items, terms, ks, nt, st);
+        return dual ? launch_dec_fd<7, true>(a, n_items, terms, ks, nt, st, inl)
+                    : launch_dec_fd<7, false>(a, n_items, terms, ks, nt, st, inl);
     return hipErrorInvalidValue;
 }
 

@@ -319,9 +319,12 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
 }
 
 // One task: item `item`, column block `wg` of one projection.  FUSED adds the hooks.
-template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool FUSED, bool PACK = false>
+// INL: the descriptor comes from `kd` (compact, in the kernel arguments), not A.desc.
+template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool FUSED, bool PACK = false,
+          bool INL = false>
 __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int tid,
-                                         char *smem, const DecSync &sy) {
+                                         char *smem, const DecSync &sy,
+                                         const DecDescK *kd = nullptr) {
     constexpr int TW = kDecWaves / KS;   // wave slots per K range
     constexpr int NU = NT == 2 ? 2 : 4;  // K blocks per tile in flight (VGPR budget)
     constexpr int XSR = 2;               // single, fmt 4: sums per thread (K / 4 <= 2048)
@@ -338,9 +341,28 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     u32x4 cpv = {0u, 0u, 0u, 0u};
     if (cp)
         cpv = reinterpret_cast<const u32x4 *>(A.cp_src + cpi)[tid & 15];
-    const DecDesc &dd = A.desc[item];
+    static_assert(!INL || (DUAL && !FUSED), "compact descriptors are gate/up only");
+    const DecDesc &dd = A.desc[INL ? 0 : item];  // not read when INL
     const int K = A.K, O = A.O;
-    const int nrow = dd.nrow, jbase = dd.jbase;
+    const void *wp[2], *sp[2];
+    int nrow, jbase;
+    if constexpr (INL) {
+        const DecDescK &k = kd[item];
+        const char *w0 = static_cast<const char *>(k.w0);
+        wp[0] = w0;
+        wp[1] = w0 + k.off[0];
+        sp[0] = w0 + k.off[1];
+        sp[1] = w0 + k.off[2];
+        nrow = k.nrow;
+        jbase = k.jbase;
+    } else {
+        wp[0] = dd.w[0];
+        wp[1] = dd.w[1];
+        sp[0] = dd.s[0];
+        sp[1] = dd.s[1];
+        nrow = dd.nrow;
+        jbase = dd.jbase;
+    }
     // wave index as a scalar: tiles and K range are then wave-uniform (SGPRs)
     const int wave = __builtin_amdgcn_readfirstlane((tid >> 6));
     const int lane = tid & 63;
@@ -356,8 +378,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
         tile[n] = DUAL ? wg * TW + slot : wg * TW * NT + slot + n * TW;
-        rw[n] = buf_rsrc(uniform_ptr(dd.w[DUAL ? n : 0]), (uint32_t)O * rowb);
-        rs[n] = buf_rsrc(uniform_ptr(dd.s[DUAL ? n : 0]), (uint32_t)O * srow);
+        rw[n] = buf_rsrc(uniform_ptr(wp[DUAL ? n : 0]), (uint32_t)O * rowb);
+        rs[n] = buf_rsrc(uniform_ptr(sp[DUAL ? n : 0]), (uint32_t)O * srow);
         vw[n] = (uint32_t)(tile[n] * 16 + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
         vs[n] = (uint32_t)(tile[n] * 16 + t) * srow +
                 (uint32_t)(FMT == 4 ? (kw0 >> 4) : (kw0 >> 5)) + 32u * (uint32_t)q;
@@ -389,7 +411,7 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
         int rr[16];  // the row map, one scalar load; picked below by uniform selects
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-            rr[i] = dd.rows[i];
+            rr[i] = INL ? (int)kd[item].rows[i] : dd.rows[i];
 #pragma unroll
         for (int u = 0; u < SR; ++u) {
             // (divisions outside the selects: a division under a condition is not

@@ -76,6 +76,23 @@ struct DecDesc {
 };
 static_assert(sizeof(DecDesc) == 256, "DecDesc layout");
 
+// A gate/up descriptor compact enough to travel in the kernel arguments, which the
+// runtime places in device memory: the workgroups' first read is then an HBM read
+// instead of a PCIe round trip to the pinned plan slot.  Used when a launch has at most
+// kDecInline items, every offset fits 32 bits and every row index 16 bits.
+struct DecDescK {
+    const void *w0;          // gate weights
+    int off[3];              // up weights, gate scales, up scales: byte offsets from w0
+    unsigned short jbase;    // first compact row of the item
+    unsigned short nrow;     // rows in the item
+    unsigned short rows[16]; // input row of item row r
+};
+static_assert(sizeof(DecDescK) == 56, "DecDescK layout");
+constexpr int kDecInline = 64;
+struct DecInline {
+    DecDescK d[kDecInline];
+};
+
 // The gate/up kernel (dual) reads the f32 input rows and splits them into `terms` bf16
 // terms in LDS; each wave computes the gate and the up tile of the same 16 columns over
 // K / ks and applies the activation in registers (ks > 1: partial sums meet in LDS).  It
@@ -99,11 +116,14 @@ constexpr int kDecMaxK = 8192;
 // 128 bytes a row (int4: 32 groups of 64; MXFP4: 128 blocks of 32).
 inline int dec_max_kr(int fmt) { return fmt == 4 ? 2048 : 4096; }
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt);
+// inl (dual only, optional): the n_items (<= kDecInline) descriptors in the compact form,
+// in host memory; copied into the kernel arguments, and desc is not read.
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
-                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st);
+                           const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
+                           const DecDescK *inl = nullptr);
 
 // Both decode projections in one cooperative launch (kern_fused.hip), the down projection
 // folding the combine into out.  Descriptors as for launch_mfma_dec, plus: pad0[0] =

@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -167,6 +168,7 @@ struct Ctx {
     int fp4act = 0;          // MXFP4 experts: 1 = quantize activations, native FP4 GEMMs
     int combine_ordered = 0;  // 1 = separate combine in the reference's order (decode too)
     int fuse = 0;            // decode: both projections in one cooperative launch
+    int dec_inline = 1;      // decode: gate/up descriptors in the kernel arguments when they fit
     // fused launch: per expert slot, gate/up tasks finished on the device (only grows) and
     // the host's running total of what was launched; err[0] = a wait gave up
     DevBuf sync;             // [16] int err + unsigned done[cap]
@@ -490,6 +492,7 @@ struct DevPlan {
     float *ent_w, *rw;
     DecDesc *gu_desc, *dn_desc;  // decode kernels: one descriptor per item of each phase
     DecDesc *dn_desc_dev;        // dn_desc in device memory (a copy the gate/up kernel makes)
+    const DecDesc *gu_host;      // gu_desc's copy in the pinned slot (host memory)
     int slot;  // plan slot index
 };
 
@@ -519,6 +522,37 @@ void build_desc(const Plan &P, const CallCfg &cc, size_t i0, size_t i1, bool dua
             }
         }
     }
+}
+
+// The compact (kernel-argument) form of gate/up descriptors d[0, n); false when some
+// descriptor does not fit it (more than kDecInline, an offset beyond 32 bits, a row index
+// beyond 16 bits).
+bool compact_desc(const DecDesc *d, int n, DecDescK *k) {
+    if (n > kDecInline)
+        return false;
+    for (int i = 0; i < n; ++i) {
+        const uintptr_t w0 = reinterpret_cast<uintptr_t>(d[i].w[0]);
+        const uintptr_t p[3] = {reinterpret_cast<uintptr_t>(d[i].w[1]),
+                                reinterpret_cast<uintptr_t>(d[i].s[0]),
+                                reinterpret_cast<uintptr_t>(d[i].s[1])};
+        k[i].w0 = d[i].w[0];
+        for (int m = 0; m < 3; ++m) {
+            const long long off = static_cast<long long>(p[m] - w0);
+            if (off < INT32_MIN || off > INT32_MAX)
+                return false;
+            k[i].off[m] = static_cast<int>(off);
+        }
+        if (d[i].jbase < 0 || d[i].jbase > 65535 || d[i].nrow < 0 || d[i].nrow > 16)
+            return false;
+        k[i].jbase = static_cast<unsigned short>(d[i].jbase);
+        k[i].nrow = static_cast<unsigned short>(d[i].nrow);
+        for (int r = 0; r < 16; ++r) {
+            if (d[i].rows[r] < 0 || d[i].rows[r] > 65535)
+                return false;
+            k[i].rows[r] = static_cast<unsigned short>(d[i].rows[r]);
+        }
+    }
+    return true;
 }
 
 int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp,
@@ -625,6 +659,7 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.rdest = reinterpret_cast<int *>(d + o_rd);
     dp.rw = reinterpret_cast<float *>(d + o_rw);
     dp.gu_desc = reinterpret_cast<DecDesc *>(d + o_dg);
+    dp.gu_host = reinterpret_cast<const DecDesc *>(h + o_dg);
     dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
     dp.dn_desc_dev = reinterpret_cast<DecDesc *>(static_cast<char *>(s.dev.p) + o_dd);
     if (!zero_copy)
@@ -801,11 +836,14 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             if (i1 <= i0)
                 continue;
             const int ncp = std::min(n_dn - copied, static_cast<int>(i1 - i0) * wgs_gu);
+            const int ni = static_cast<int>(i1 - i0);
+            DecDescK kd[kDecInline];
+            const bool inl = C.dec_inline && compact_desc(dp.gu_host + (i0 - cc.gu.it0), ni, kd);
             HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.nt,
-                                    dp.gu_desc + (i0 - cc.gu.it0), static_cast<int>(i1 - i0), in,
-                                    nullptr, nullptr, C.Ph.p, static_cast<float *>(C.HP.p),
-                                    nullptr, D, I, rcap, rmax_gu, act, a, b, false, pk_gu,
-                                    dp.dn_desc + copied, dp.dn_desc_dev + copied, ncp, st));
+                                    dp.gu_desc + (i0 - cc.gu.it0), ni, in, nullptr, nullptr,
+                                    C.Ph.p, static_cast<float *>(C.HP.p), nullptr, D, I, rcap,
+                                    rmax_gu, act, a, b, false, pk_gu, dp.dn_desc + copied,
+                                    dp.dn_desc_dev + copied, ncp, st, inl ? kd : nullptr));
             copied += ncp;
             C.stats[13] += 1;
         }
@@ -1039,6 +1077,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         gemm_set_persistent(value != 0);
     } else if (k == "fuse") {
         C.fuse = value ? 1 : 0;
+    } else if (k == "dec_inline") {
+        C.dec_inline = value ? 1 : 0;
     } else if (k == "combine_ordered") {
         C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {

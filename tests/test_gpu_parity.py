@@ -205,6 +205,28 @@ def test_decode_k_split_parity(hip, orc, ci, ks):
     assert err < TOL_F32
 
 
+@pytest.mark.parametrize("inline", [0, 1])
+@pytest.mark.parametrize("ci", [1, 3, 7, "many"])
+def test_decode_descriptor_paths(hip, orc, ci, inline):
+    """Gate/up descriptors in the kernel arguments (dec_inline 1, default) or read from
+    the pinned plan slot (0); 'many' has 70 items, past the 64 the arguments carry, so
+    it takes the slot either way."""
+    case = (4, 512, 256, [1] * 70, 16, 1, 7.0, 0.0, (), 0) if ci == "many" else DEV_CASES[ci]
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("dec_inline", inline, ci)
+    rng = np.random.default_rng(D * 43 + I + inline)
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    assert hip.set_option("dec_inline", inline)
+    try:
+        got = run_dev(hip, c, act, a, b)
+    finally:
+        hip.set_option("dec_inline", 1)
+    exp = oracle_out(orc, c, act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err", err)
+    assert err < TOL_F32
+
+
 @pytest.mark.parametrize("case", DEV_CASES[::2])
 def test_moe_block_host_parity(hip, orc, case):
     fmt, D, I, nr, S, act, a, b, nulls, bad = case
