@@ -132,6 +132,28 @@ int mvllm_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int
                        int *xoff, int *nr, int *rows, float *rw, int cap_experts, int cap_rows,
                        int *n_rows);
 
+/* ---- the same routing on the device, for callers that keep the router output in HBM:
+ *      moe_topk (src/model/ops.cpp:860-889) of every token, and mvllm_moe_segments.
+ *      Bit-exact with the host functions.  Enqueued on `stream` (NULL: the null stream);
+ *      both return 1 when enqueued, 0 on bad arguments (mvllm_hip_last_error). ---- */
+
+/* choice, mix (or NULL: weights from choice): device f32 [n_tok][n_exp]; idx int32 and
+ * wt f32 [n_tok][k] on the device, row t equal to moe_topk(choice + t*n_exp, n_exp, k,
+ * ..., mix ? mix + t*n_exp : NULL).  1 <= k <= 64, k <= n_exp <= 4096; scores must not
+ * be NaN (the reference's sort has no order for them). */
+int mvllm_hip_moe_topk_dev(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                           int *idx, float *wt, void *stream);
+
+/* mvllm_moe_segments of device idx/wt [n_tok][topk] (ids < n_exp; negative ids are
+ * skipped as the reference does).  Device outputs eids/xoff/nr [cap_experts], rows/rw
+ * [cap_rows] and counts int32[2] = {nb, n_rows}, or {-1, -1} when cap_rows is short or
+ * an id >= n_exp (the other outputs are then undefined).  The union keeps its
+ * cap_experts smallest ids, as mvllm_moe_union_ids does.  work: device int32 scratch of
+ * 2 * n_exp + 1 entries; calls that share a work buffer must not overlap. */
+int mvllm_hip_moe_segments_dev(const int *idx, const float *wt, int n_tok, int topk, int n_exp,
+                               int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
+                               int cap_experts, int cap_rows, int *counts, void *stream);
+
 /* Expert blob geometry (byte offsets of the six pieces inside one expert blob):
  * fmt 4 = GLM gate_p|gate_s|up_p|up_s|down_p|down_s (src/model/glm53.cpp:56-78,
  * 116-132); fmt 7 = K3 w1p|w1s|w2p|w2s|w3p|w3s with gate=w1, down=w2, up=w3

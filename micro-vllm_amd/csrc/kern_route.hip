@@ -1,0 +1,266 @@
+// kern_route.hip -- the routing in front of the expert block, on the device: moe_topk of
+// every token (src/model/ops.cpp:860-889), then the moe_block segments of one batched
+// call (the union of src/model/ops.cpp:1082-1099 and the per-expert gather of
+// src/model/glm53.cpp:1938-1971 / src/model/kimi_k3.cpp:2009-2050).  Integer work and a
+// few f32 additions and divisions in the reference's order: bit-exact.
+//
+//   k_moe_topk      one wave per token: k rounds of a wave-wide argmax under the
+//                   reference's order (larger score first, lower index on ties), then the
+//                   weights summed in pick order by every lane alike;
+//   k_seg_count     per (token, slot): the expert's count of tokens whose summed weight
+//                   is non-zero, and its presence (union membership: any slot);
+//   k_seg_scan      one workgroup: experts in ascending id -> positions, row offsets,
+//                   the capacity checks;
+//   k_seg_rows      one workgroup per kept expert: its tokens in ascending order by a
+//                   block-wide scan, written at the expert's row offset.
+#include "moe_internal.h"
+
+#include <algorithm>
+
+namespace mvllm_hip {
+
+// a ranks before b: larger score first, lower index on ties (the reference comparator;
+// -0 and +0 tie).  Scores are not NaN (the reference's sort has no order for NaN).
+__device__ __forceinline__ bool rank_before(float va, int a, float vb, int b) {
+    return va == vb ? a < b : va > vb;
+}
+
+constexpr int kTopkWaves = 4;
+
+__global__ __launch_bounds__(64 * kTopkWaves) void k_moe_topk(const float *choice,
+                                                                const float *mix, int n_tok,
+                                                                int n_exp, int k, int *idx,
+                                                                float *wt) {
+    const int tok = blockIdx.x * kTopkWaves + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (tok >= n_tok)  // wave-uniform
+        return;
+    const float *row = choice + (size_t)tok * n_exp;
+    uint64_t taken = 0;  // bit s: element lane + 64 s is picked (n_exp <= 4096)
+    int mine = -1;       // lane i < k: the i-th pick
+    for (int i = 0; i < k; ++i) {
+        float bv = 0.f;
+        int bi = -1;
+        for (int s = 0; lane + 64 * s < n_exp; ++s) {
+            const int j = lane + 64 * s;
+            if ((taken >> s) & 1u)
+                continue;
+            const float v = row[j];
+            if (bi < 0 || rank_before(v, j, bv, bi)) {
+                bv = v;
+                bi = j;
+            }
+        }
+        // the order is total on the candidates, so any reduction tree finds the same one
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int oi = __shfl_xor(bi, off);
+            if (oi >= 0 && (bi < 0 || rank_before(ov, oi, bv, bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane)
+            taken |= 1ull << (bi >> 6);
+        if (lane == i)
+            mine = bi;
+    }
+    // weights: clipped at 0, summed in pick order (every lane adds the same sequence)
+    float w = 0.f;
+    if (lane < k) {
+        w = mix ? mix[(size_t)tok * n_exp + mine] : row[mine];
+        if (w < 0.f)
+            w = 0.f;
+    }
+    float sum = 0.f;
+    for (int i = 0; i < k; ++i)
+        sum += __shfl(w, i);
+    if (lane < k) {
+        idx[(size_t)tok * k + lane] = mine;
+        wt[(size_t)tok * k + lane] = sum > 0.f ? w / sum : 1.f / (float)k;
+    }
+}
+
+// work layout (ints): cnt[n_exp] | pos[n_exp] (0 = absent, 1 = present; the scan turns
+// it into the expert's position or -1) | flag (1: an id >= n_exp was seen)
+__global__ __launch_bounds__(256) void k_seg_zero(int *work, int n) {
+    for (int i = blockIdx.x * 256 + (int)threadIdx.x; i < n; i += (int)gridDim.x * 256)
+        work[i] = 0;
+}
+
+// Summed weight of token c for expert e over its slots, in slot order from 0 (the
+// reference's wsum), and whether any slot names e.
+__device__ __forceinline__ float slot_wsum(const int *idx, const float *wt, int c, int topk,
+                                           int e, bool &named) {
+    float ws = 0.f;
+    named = false;
+    for (int t = 0; t < topk; ++t)
+        if (idx[(size_t)c * topk + t] == e) {
+            ws += wt[(size_t)c * topk + t];
+            named = true;
+        }
+    return ws;
+}
+
+__global__ __launch_bounds__(256) void k_seg_count(const int *idx, const float *wt, int n_tok,
+                                                   int topk, int n_exp, int *work) {
+    const int i = blockIdx.x * 256 + (int)threadIdx.x;
+    if (i >= n_tok * topk)
+        return;
+    const int c = i / topk, t = i - c * topk;
+    const int e = idx[i];
+    if (e < 0)
+        return;
+    if (e >= n_exp) {
+        work[2 * n_exp] = 1;
+        return;
+    }
+    // only the token's first slot naming e counts the token
+    for (int u = 0; u < t; ++u)
+        if (idx[(size_t)c * topk + u] == e)
+            return;
+    bool named;
+    const float ws = slot_wsum(idx, wt, c, topk, e, named);
+    work[n_exp + e] = 1;
+    if (ws != 0.f)
+        atomicAdd(work + e, 1);
+}
+
+// One workgroup of 1024: experts in ascending id.  counts = {nb, rows}, or {-1, -1} when
+// cap_rows is short or an id is out of range.  The union keeps its cap_experts smallest
+// ids, as the reference's union does.
+__global__ __launch_bounds__(1024) void k_seg_scan(int n_exp, int *work, int cap_experts,
+                                                   int cap_rows, int *eids, int *xoff, int *nr,
+                                                   int *counts) {
+    __shared__ int wsum_p[16], wsum_r[16];
+    __shared__ int base_p, base_r;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        base_p = 0;
+        base_r = 0;
+    }
+    __syncthreads();
+    for (int e0 = 0; e0 < n_exp; e0 += 1024) {
+        const int e = e0 + tid;
+        const int p = e < n_exp ? work[n_exp + e] : 0;
+        const int r = e < n_exp && p ? work[e] : 0;
+        // inclusive scans within the wave
+        int sp = p, sr = r;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int up = __shfl_up(sp, off), ur = __shfl_up(sr, off);
+            if (lane >= off) {
+                sp += up;
+                sr += ur;
+            }
+        }
+        if (lane == 63) {
+            wsum_p[wave] = sp;
+            wsum_r[wave] = sr;
+        }
+        __syncthreads();
+        int bp = base_p, br = base_r;
+        for (int w = 0; w < wave; ++w) {
+            bp += wsum_p[w];
+            br += wsum_r[w];
+        }
+        const int ui = bp + sp - p;  // exclusive: position among present experts
+        const int ro = br + sr - r;  // rows before this expert
+        if (e < n_exp) {
+            const bool kept = p && ui < cap_experts;
+            work[n_exp + e] = kept ? ui : -1;
+            if (kept) {
+                eids[ui] = e;
+                xoff[ui] = ro;
+                nr[ui] = r;
+            }
+        }
+        __syncthreads();
+        if (tid == 1023) {
+            base_p = bp + sp;
+            base_r = br + sr;
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        // rows of the kept experts only: the dropped ones have the larger ids
+        int nb = base_p < cap_experts ? base_p : cap_experts;
+        int rows = 0;
+        if (base_p <= cap_experts) {
+            rows = base_r;
+        } else {
+            for (int e = 0; e < n_exp; ++e)  // truncated union (rare): count again
+                if (work[n_exp + e] >= 0)
+                    rows += work[e];
+        }
+        const bool bad = work[2 * n_exp] != 0 || rows > cap_rows;
+        counts[0] = bad ? -1 : nb;
+        counts[1] = bad ? -1 : rows;
+    }
+}
+
+// One workgroup per expert id: the kept ones write their tokens (ascending) and sums.
+__global__ __launch_bounds__(256) void k_seg_rows(const int *idx, const float *wt, int n_tok,
+                                                  int topk, int n_exp, const int *work,
+                                                  const int *xoff, const int *counts,
+                                                  int *rows, float *rw) {
+    __shared__ int wcnt[4];
+    const int e = blockIdx.x;
+    const int ui = work[n_exp + e];
+    if (ui < 0 || counts[0] < 0)  // workgroup-uniform
+        return;
+    const int tid = (int)threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int j = xoff[ui];
+    for (int c0 = 0; c0 < n_tok; c0 += 256) {
+        const int c = c0 + tid;
+        bool named = false;
+        const float ws = c < n_tok ? slot_wsum(idx, wt, c, topk, e, named) : 0.f;
+        const bool take = c < n_tok && ws != 0.f;
+        const uint64_t m = __ballot(take);
+        const int before = __popcll(m & ((1ull << lane) - 1ull));
+        if (lane == 0)
+            wcnt[wave] = __popcll(m);
+        __syncthreads();
+        int off = j;
+        for (int w = 0; w < wave; ++w)
+            off += wcnt[w];
+        if (take) {
+            rows[off + before] = c;
+            rw[off + before] = ws;
+        }
+        const int tot = wcnt[0] + wcnt[1] + wcnt[2] + wcnt[3];
+        __syncthreads();
+        j += tot;
+    }
+}
+
+hipError_t launch_moe_topk(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                           int *idx, float *wt, hipStream_t st) {
+    if (n_tok < 1 || n_exp < 1 || n_exp > kRouteMaxExperts || k < 1 || k > 64 || k > n_exp)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_moe_topk, dim3((unsigned)((n_tok + kTopkWaves - 1) / kTopkWaves)),
+                       dim3(64 * kTopkWaves), 0, st, choice, mix, n_tok, n_exp, k, idx, wt);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int n_exp,
+                               int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
+                               int cap_experts, int cap_rows, int *counts, hipStream_t st) {
+    if (n_tok < 1 || topk < 1 || n_exp < 1 || cap_experts < 1 || cap_rows < 1 ||
+        (long long)n_tok * topk > (1ll << 30))
+        return hipErrorInvalidValue;
+    const int nw = 2 * n_exp + 1;
+    hipLaunchKernelGGL(k_seg_zero, dim3((unsigned)std::min((nw + 255) / 256, 1024)), dim3(256), 0,
+                       st, work, nw);
+    const int pairs = n_tok * topk;
+    hipLaunchKernelGGL(k_seg_count, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, st, idx,
+                       wt, n_tok, topk, n_exp, work);
+    hipLaunchKernelGGL(k_seg_scan, dim3(1), dim3(1024), 0, st, n_exp, work, cap_experts, cap_rows,
+                       eids, xoff, nr, counts);
+    hipLaunchKernelGGL(k_seg_rows, dim3((unsigned)n_exp), dim3(256), 0, st, idx, wt, n_tok, topk,
+                       n_exp, work, xoff, counts, rows, rw);
+    return hipGetLastError();
+}
+
+}  // namespace mvllm_hip

@@ -60,6 +60,15 @@ hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, i
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st, const int *rows_map = nullptr);
 
+// Routing on the device (kern_route.hip): moe_topk per token, and the segments of one
+// batched moe_block call.  Bit-exact with the host versions.
+constexpr int kRouteMaxExperts = 4096;
+hipError_t launch_moe_topk(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                           int *idx, float *wt, hipStream_t st);
+hipError_t launch_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int n_exp,
+                               int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
+                               int cap_experts, int cap_rows, int *counts, hipStream_t st);
+
 // Matrix-core decode path (kern_mfma.hip).  One descriptor per item (up to rmax <= 16
 // rows of one expert), built by the host: everything a workgroup needs before its first
 // weight load, so one dependent read starts both the weight stream and the activation

@@ -1487,6 +1487,36 @@ int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, i
     return 1;
 }
 
+int mvllm_hip_moe_topk_dev(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                           int *idx, float *wt, void *stream) {
+    Ctx &C = ctx();
+    set_err("");
+    if (!C.ready || !choice || !idx || !wt || n_tok < 1 || n_exp < 1 ||
+        n_exp > kRouteMaxExperts || k < 1 || k > 64 || k > n_exp) {
+        set_err("moe_topk_dev: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_moe_topk(choice, mix, n_tok, n_exp, k, idx, wt,
+                            static_cast<hipStream_t>(stream)));
+    return 1;
+}
+
+int mvllm_hip_moe_segments_dev(const int *idx, const float *wt, int n_tok, int topk, int n_exp,
+                               int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
+                               int cap_experts, int cap_rows, int *counts, void *stream) {
+    Ctx &C = ctx();
+    set_err("");
+    if (!C.ready || !idx || !wt || !work || !eids || !xoff || !nr || !rows || !rw || !counts ||
+        n_tok < 1 || topk < 1 || n_exp < 1 || cap_experts < 1 || cap_rows < 1 ||
+        (long long)n_tok * topk > (1ll << 30)) {
+        set_err("moe_segments_dev: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_moe_segments(idx, wt, n_tok, topk, n_exp, work, eids, xoff, nr, rows, rw,
+                                cap_experts, cap_rows, counts, static_cast<hipStream_t>(stream)));
+    return 1;
+}
+
 int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
                              uint8_t *scales_dev) {
     Ctx &C = ctx();

@@ -57,6 +57,9 @@ _SIGS = {
     "mvllm_hip_stats_reset": (None, []),
     "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
     "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
+    "mvllm_hip_moe_topk_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
+    "mvllm_hip_moe_segments_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p,
+                                        _p]),
     "mvllm_hip_membench": (_i, [_i, _p, _p, _sz, _i, _i, _p]),
 }
 
@@ -208,6 +211,26 @@ def stats_reset():
 def dequant(fmt, packed_dev, scales_dev, O, K, w_dev):
     _check(lib().mvllm_hip_dequant(fmt, _ptr(packed_dev), _ptr(scales_dev), O, K, _ptr(w_dev)),
            "mvllm_hip_dequant")
+
+
+def _stream(stream):
+    return None if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+
+
+def moe_topk_dev(choice, mix, n_tok, n_exp, k, idx, wt, stream=None):
+    """moe_topk of every token on the device (see mvllm_hip_moe_topk_dev); enqueued."""
+    _check(lib().mvllm_hip_moe_topk_dev(_ptr(choice), _ptr(mix), n_tok, n_exp, k, _ptr(idx),
+                                        _ptr(wt), _stream(stream)), "mvllm_hip_moe_topk_dev")
+
+
+def moe_segments_dev(idx, wt, n_tok, topk, n_exp, work, eids, xoff, nr, rows, rw, counts,
+                     stream=None):
+    """mvllm_moe_segments on the device (see mvllm_hip_moe_segments_dev); enqueued.
+    Capacities are the lengths of eids and rows."""
+    _check(lib().mvllm_hip_moe_segments_dev(_ptr(idx), _ptr(wt), n_tok, topk, n_exp, _ptr(work),
+                                            _ptr(eids), _ptr(xoff), _ptr(nr), _ptr(rows),
+                                            _ptr(rw), len(eids), len(rows), _ptr(counts),
+                                            _stream(stream)), "mvllm_hip_moe_segments_dev")
 
 
 def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):
