@@ -230,9 +230,16 @@ def main():
             sizes[mib] = {"us": round(t * 1e3, 2), "gbps": round(nb / t / 1e6, 1)}
             log(f"  read {mib:5d} MiB in one launch: {t*1e3:8.2f} us, {nb / t / 1e6:7.0f} GB/s")
 
+    # the routing in front of the block on the device (moe_topk of every token, then the
+    # batched call's segments) for this layer shape, and its host counterpart
+    route, scores = route_timing(torch, mvllm_hip, T, E, k)
+    log(f"device routing (T={T}, E={E}, k={k}): {route['us_per_call']:.2f} us per call")
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, args.cpu_seconds)
+        route["cpu_us_per_call"], route["cpu_kind"] = cpu_route_baseline(np, scores, k)
+        log(f"host routing: {route['cpu_us_per_call']:.1f} us per call ({route['cpu_kind']})")
 
     rec = {
         "metric": "moe_block tokens/s (decode), effective weight GB/s",
@@ -265,8 +272,66 @@ def main():
         "phases_us": {"gate_up": round(ms_gu * 1e3, 3), "down": round(ms_dn * 1e3, 3),
                       "combine": round(ms_cb * 1e3, 3)},
         "cpu_baseline": cpu,
+        "route": route,
     }
     print(json.dumps(rec), flush=True)
+
+
+def route_timing(torch, mvllm_hip, T, E, k, reps=200):
+    """GPU time per call of mvllm_hip_moe_topk_dev + mvllm_hip_moe_segments_dev on N(0,1)
+    router scores (weights from their sigmoid), HIP events on the null stream the calls
+    are enqueued on.  Returns the record and the scores (for the host baseline)."""
+    g = torch.Generator(device="cuda").manual_seed(7)
+    choice = torch.randn((T, E), device="cuda", generator=g)
+    mix = torch.sigmoid(choice)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    idx, wt = torch.empty((T, k), **i32), torch.empty((T, k), dtype=torch.float32, device="cuda")
+    work, counts = torch.empty(2 * E + 1, **i32), torch.empty(2, **i32)
+    eids, xoff, nr = (torch.empty(E, **i32) for _ in range(3))
+    rows, rw = torch.empty(T * k, **i32), torch.empty(T * k, dtype=torch.float32, device="cuda")
+    a = [x.data_ptr() for x in (choice, mix, idx, wt, work, eids, xoff, nr, rows, rw, counts)]
+    L = mvllm_hip.lib()
+
+    def one():
+        return (L.mvllm_hip_moe_topk_dev(a[0], a[1], T, E, k, a[2], a[3], None) and
+                L.mvllm_hip_moe_segments_dev(a[2], a[3], T, k, E, a[4], a[5], a[6], a[7], a[8],
+                                             a[9], E, T * k, a[10], None))
+    for _ in range(10):
+        if not one():
+            raise SystemExit("device routing failed: " + L.mvllm_hip_last_error().decode())
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        one()
+    e1.record()
+    torch.cuda.synchronize()
+    nb, n_rows = (int(v) for v in counts.cpu())
+    rec = {"us_per_call": round(e0.elapsed_time(e1) / reps * 1e3, 3), "n_tok": T, "n_exp": E,
+           "k": k, "experts": nb, "rows": n_rows, "launches_per_call": 5}
+    return rec, (choice.cpu().numpy(), mix.cpu().numpy())
+
+
+def cpu_route_baseline(np, scores, k, budget_s=2.0):
+    """The host routing on the same scores: moe_topk per token (oracle/_ref build when
+    present, else the C restatement) and the segments (C restatement), one thread."""
+    import oracle
+    kind = "reference" if oracle.have_ref() else "port"
+    topk = oracle.CpuMoe("ref" if kind == "reference" else "oracle")
+    seg = oracle.CpuMoe("oracle")
+    choice, mix = scores
+    T, E = choice.shape
+    idx, wt = np.empty((T, k), np.int32), np.empty((T, k), np.float32)
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        for t in range(T):
+            _, idx[t], wt[t] = topk.moe_topk(choice[t], k, mix[t])
+        seg.moe_segments(idx, wt, T, k, E)
+        calls += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    return round((time.perf_counter() - t0) / calls * 1e6, 1), \
+        f"{kind}; moe_topk per token through ctypes (~1 us call overhead each), then the segments"
 
 
 def staged(args, np, torch, mvllm_hip, synth, cfg, T):

@@ -12,7 +12,7 @@
 //   k_seg_scan      one workgroup: experts in ascending id -> positions, row offsets,
 //                   the capacity checks;
 //   k_seg_rows      one workgroup per kept expert: its tokens in ascending order by a
-//                   block-wide scan, written at the expert's row offset.
+//                   ballot per 256 tokens, written at the expert's row offset.
 #include "moe_internal.h"
 
 #include <algorithm>
@@ -27,6 +27,9 @@ __device__ __forceinline__ bool rank_before(float va, int a, float vb, int b) {
 
 constexpr int kTopkWaves = 4;
 
+// NV > 0: the lane's scores (elements lane + 64 s, s < NV) stay in registers for all k
+// rounds (n_exp <= 64 NV); NV = 0 reads them again each round (up to 4096 experts).
+template <int NV>
 __global__ __launch_bounds__(64 * kTopkWaves) void k_moe_topk(const float *choice,
                                                                 const float *mix, int n_tok,
                                                                 int n_exp, int k, int *idx,
@@ -36,19 +39,34 @@ __global__ __launch_bounds__(64 * kTopkWaves) void k_moe_topk(const float *choic
     if (tok >= n_tok)  // wave-uniform
         return;
     const float *row = choice + (size_t)tok * n_exp;
+    float cv[NV > 0 ? NV : 1];
+#pragma unroll
+    for (int s = 0; s < NV; ++s)
+        cv[s] = lane + 64 * s < n_exp ? row[lane + 64 * s] : 0.f;
     uint64_t taken = 0;  // bit s: element lane + 64 s is picked (n_exp <= 4096)
     int mine = -1;       // lane i < k: the i-th pick
     for (int i = 0; i < k; ++i) {
         float bv = 0.f;
         int bi = -1;
-        for (int s = 0; lane + 64 * s < n_exp; ++s) {
-            const int j = lane + 64 * s;
-            if ((taken >> s) & 1u)
-                continue;
-            const float v = row[j];
-            if (bi < 0 || rank_before(v, j, bv, bi)) {
-                bv = v;
-                bi = j;
+        if constexpr (NV > 0) {
+#pragma unroll
+            for (int s = 0; s < NV; ++s) {
+                const int j = lane + 64 * s;
+                if (j < n_exp && !((taken >> s) & 1u) && (bi < 0 || rank_before(cv[s], j, bv, bi))) {
+                    bv = cv[s];
+                    bi = j;
+                }
+            }
+        } else {
+            for (int s = 0; lane + 64 * s < n_exp; ++s) {
+                const int j = lane + 64 * s;
+                if ((taken >> s) & 1u)
+                    continue;
+                const float v = row[j];
+                if (bi < 0 || rank_before(v, j, bv, bi)) {
+                    bv = v;
+                    bi = j;
+                }
             }
         }
         // the order is total on the candidates, so any reduction tree finds the same one
@@ -89,20 +107,23 @@ __global__ __launch_bounds__(256) void k_seg_zero(int *work, int n) {
         work[i] = 0;
 }
 
-// Summed weight of token c for expert e over its slots, in slot order from 0 (the
-// reference's wsum), and whether any slot names e.
+// Summed weight of token c for expert e over its slots, in slot order from +0 (the
+// reference's wsum).  Slots naming another expert add +0, which leaves the sum as it is:
+// a sum started at +0 never becomes -0, and x + 0 = x otherwise (inf and NaN included).
+// So every slot is loaded unconditionally and the loads issue together.
 __device__ __forceinline__ float slot_wsum(const int *idx, const float *wt, int c, int topk,
-                                           int e, bool &named) {
+                                           int e) {
     float ws = 0.f;
-    named = false;
-    for (int t = 0; t < topk; ++t)
-        if (idx[(size_t)c * topk + t] == e) {
-            ws += wt[(size_t)c * topk + t];
-            named = true;
-        }
+    for (int t = 0; t < topk; ++t) {
+        const int id = idx[(size_t)c * topk + t];
+        const float w = wt[(size_t)c * topk + t];
+        ws += id == e ? w : 0.f;
+    }
     return ws;
 }
 
+// One thread per (token, slot): the token's first slot naming an expert counts the token
+// for it when the summed weight is non-zero; every named expert is present.
 __global__ __launch_bounds__(256) void k_seg_count(const int *idx, const float *wt, int n_tok,
                                                    int topk, int n_exp, int *work) {
     const int i = blockIdx.x * 256 + (int)threadIdx.x;
@@ -116,12 +137,12 @@ __global__ __launch_bounds__(256) void k_seg_count(const int *idx, const float *
         work[2 * n_exp] = 1;
         return;
     }
-    // only the token's first slot naming e counts the token
+    bool first = true;
     for (int u = 0; u < t; ++u)
-        if (idx[(size_t)c * topk + u] == e)
-            return;
-    bool named;
-    const float ws = slot_wsum(idx, wt, c, topk, e, named);
+        first = first && idx[(size_t)c * topk + u] != e;
+    if (!first)
+        return;
+    const float ws = slot_wsum(idx, wt, c, topk, e);
     work[n_exp + e] = 1;
     if (ws != 0.f)
         atomicAdd(work + e, 1);
@@ -200,7 +221,9 @@ __global__ __launch_bounds__(1024) void k_seg_scan(int n_exp, int *work, int cap
     }
 }
 
-// One workgroup per expert id: the kept ones write their tokens (ascending) and sums.
+// One workgroup per expert id: the kept ones write their tokens (ascending) and sums,
+// 256 tokens at a time placed by a ballot.  Weights are loaded only for the slots that
+// name the expert (a pass loading every slot's weight measured 50 % slower here).
 __global__ __launch_bounds__(256) void k_seg_rows(const int *idx, const float *wt, int n_tok,
                                                   int topk, int n_exp, const int *work,
                                                   const int *xoff, const int *counts,
@@ -214,8 +237,11 @@ __global__ __launch_bounds__(256) void k_seg_rows(const int *idx, const float *w
     int j = xoff[ui];
     for (int c0 = 0; c0 < n_tok; c0 += 256) {
         const int c = c0 + tid;
-        bool named = false;
-        const float ws = c < n_tok ? slot_wsum(idx, wt, c, topk, e, named) : 0.f;
+        float ws = 0.f;  // the reference's wsum: matching slots in slot order from +0
+        if (c < n_tok)
+            for (int t = 0; t < topk; ++t)
+                if (idx[(size_t)c * topk + t] == e)
+                    ws += wt[(size_t)c * topk + t];
         const bool take = c < n_tok && ws != 0.f;
         const uint64_t m = __ballot(take);
         const int before = __popcll(m & ((1ull << lane) - 1ull));
@@ -239,8 +265,14 @@ hipError_t launch_moe_topk(const float *choice, const float *mix, int n_tok, int
                            int *idx, float *wt, hipStream_t st) {
     if (n_tok < 1 || n_exp < 1 || n_exp > kRouteMaxExperts || k < 1 || k > 64 || k > n_exp)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_moe_topk, dim3((unsigned)((n_tok + kTopkWaves - 1) / kTopkWaves)),
-                       dim3(64 * kTopkWaves), 0, st, choice, mix, n_tok, n_exp, k, idx, wt);
+    const dim3 grid((unsigned)((n_tok + kTopkWaves - 1) / kTopkWaves)), block(64 * kTopkWaves);
+    const int nv = (n_exp + 63) / 64;
+    if (nv <= 2)
+        hipLaunchKernelGGL(k_moe_topk<2>, grid, block, 0, st, choice, mix, n_tok, n_exp, k, idx, wt);
+    else if (nv <= 8)
+        hipLaunchKernelGGL(k_moe_topk<8>, grid, block, 0, st, choice, mix, n_tok, n_exp, k, idx, wt);
+    else
+        hipLaunchKernelGGL(k_moe_topk<0>, grid, block, 0, st, choice, mix, n_tok, n_exp, k, idx, wt);
     return hipGetLastError();
 }
 
