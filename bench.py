@@ -278,9 +278,10 @@ def main():
 
 
 def route_timing(torch, mvllm_hip, T, E, k, reps=200):
-    """GPU time per call of mvllm_hip_moe_topk_dev + mvllm_hip_moe_segments_dev on N(0,1)
-    router scores (weights from their sigmoid), HIP events on the null stream the calls
-    are enqueued on.  Returns the record and the scores (for the host baseline)."""
+    """GPU time per call of mvllm_hip_moe_route_dev (moe_topk of every token, then the
+    segments) on N(0,1) router scores (weights from their sigmoid), HIP events on the
+    null stream the calls are enqueued on.  Returns the record and the scores (for the
+    host baseline)."""
     g = torch.Generator(device="cuda").manual_seed(7)
     choice = torch.randn((T, E), device="cuda", generator=g)
     mix = torch.sigmoid(choice)
@@ -293,9 +294,8 @@ def route_timing(torch, mvllm_hip, T, E, k, reps=200):
     L = mvllm_hip.lib()
 
     def one():
-        return (L.mvllm_hip_moe_topk_dev(a[0], a[1], T, E, k, a[2], a[3], None) and
-                L.mvllm_hip_moe_segments_dev(a[2], a[3], T, k, E, a[4], a[5], a[6], a[7], a[8],
-                                             a[9], E, T * k, a[10], None))
+        return L.mvllm_hip_moe_route_dev(a[0], a[1], T, E, k, a[2], a[3], a[4], a[5], a[6], a[7],
+                                         a[8], a[9], E, T * k, a[10], None)
     for _ in range(10):
         if not one():
             raise SystemExit("device routing failed: " + L.mvllm_hip_last_error().decode())

@@ -154,6 +154,13 @@ int mvllm_hip_moe_segments_dev(const int *idx, const float *wt, int n_tok, int t
                                int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
                                int cap_experts, int cap_rows, int *counts, void *stream);
 
+/* Both in one call: mvllm_hip_moe_topk_dev, then mvllm_hip_moe_segments_dev of its
+ * idx / wt (same arguments, same results; five launches). */
+int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                            int *idx, float *wt, int *work, int *eids, int *xoff, int *nr,
+                            int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
+                            void *stream);
+
 /* Expert blob geometry (byte offsets of the six pieces inside one expert blob):
  * fmt 4 = GLM gate_p|gate_s|up_p|up_s|down_p|down_s (src/model/glm53.cpp:56-78,
  * 116-132); fmt 7 = K3 w1p|w1s|w2p|w2s|w3p|w3s with gate=w1, down=w2, up=w3

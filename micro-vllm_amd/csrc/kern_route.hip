@@ -295,4 +295,15 @@ hipError_t launch_moe_segments(const int *idx, const float *wt, int n_tok, int t
     return hipGetLastError();
 }
 
+hipError_t launch_moe_route(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                            int *idx, float *wt, int *work, int *eids, int *xoff, int *nr,
+                            int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
+                            hipStream_t st) {
+    hipError_t e = launch_moe_topk(choice, mix, n_tok, n_exp, k, idx, wt, st);
+    if (e != hipSuccess)
+        return e;
+    return launch_moe_segments(idx, wt, n_tok, k, n_exp, work, eids, xoff, nr, rows, rw,
+                               cap_experts, cap_rows, counts, st);
+}
+
 }  // namespace mvllm_hip

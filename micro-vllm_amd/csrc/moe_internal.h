@@ -68,6 +68,11 @@ hipError_t launch_moe_topk(const float *choice, const float *mix, int n_tok, int
 hipError_t launch_moe_segments(const int *idx, const float *wt, int n_tok, int topk, int n_exp,
                                int *work, int *eids, int *xoff, int *nr, int *rows, float *rw,
                                int cap_experts, int cap_rows, int *counts, hipStream_t st);
+// moe_topk then the segments, on one stream.
+hipError_t launch_moe_route(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                            int *idx, float *wt, int *work, int *eids, int *xoff, int *nr,
+                            int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
+                            hipStream_t st);
 
 // Matrix-core decode path (kern_mfma.hip).  One descriptor per item (up to rmax <= 16
 // rows of one expert), built by the host: everything a workgroup needs before its first

@@ -1079,6 +1079,7 @@ int mvllm_hip_set_option(const char *key, long long value) {
         C.fuse = value ? 1 : 0;
     } else if (k == "dec_inline") {
         C.dec_inline = value ? 1 : 0;
+
     } else if (k == "combine_ordered") {
         C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {
@@ -1514,6 +1515,23 @@ int mvllm_hip_moe_segments_dev(const int *idx, const float *wt, int n_tok, int t
     }
     HIP_TRY(launch_moe_segments(idx, wt, n_tok, topk, n_exp, work, eids, xoff, nr, rows, rw,
                                 cap_experts, cap_rows, counts, static_cast<hipStream_t>(stream)));
+    return 1;
+}
+
+int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, int n_exp, int k,
+                            int *idx, float *wt, int *work, int *eids, int *xoff, int *nr,
+                            int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
+                            void *stream) {
+    Ctx &C = ctx();
+    set_err("");
+    if (!C.ready || !choice || !idx || !wt || !work || !eids || !xoff || !nr || !rows || !rw ||
+        !counts || n_tok < 1 || n_exp < 1 || n_exp > kRouteMaxExperts || k < 1 || k > 64 ||
+        k > n_exp || cap_experts < 1 || cap_rows < 1 || (long long)n_tok * k > (1ll << 30)) {
+        set_err("moe_route_dev: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_moe_route(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, rows, rw,
+                             cap_experts, cap_rows, counts, static_cast<hipStream_t>(stream)));
     return 1;
 }
 

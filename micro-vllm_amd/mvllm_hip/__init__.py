@@ -60,6 +60,8 @@ _SIGS = {
     "mvllm_hip_moe_topk_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "mvllm_hip_moe_segments_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p,
                                         _p]),
+    "mvllm_hip_moe_route_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i,
+                                     _p, _p]),
     "mvllm_hip_membench": (_i, [_i, _p, _p, _sz, _i, _i, _p]),
 }
 
@@ -231,6 +233,15 @@ def moe_segments_dev(idx, wt, n_tok, topk, n_exp, work, eids, xoff, nr, rows, rw
                                             _ptr(eids), _ptr(xoff), _ptr(nr), _ptr(rows),
                                             _ptr(rw), len(eids), len(rows), _ptr(counts),
                                             _stream(stream)), "mvllm_hip_moe_segments_dev")
+
+
+def moe_route_dev(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, rows, rw,
+                  counts, stream=None):
+    """moe_topk_dev then moe_segments_dev in one call (see mvllm_hip_moe_route_dev)."""
+    _check(lib().mvllm_hip_moe_route_dev(_ptr(choice), _ptr(mix), n_tok, n_exp, k, _ptr(idx),
+                                         _ptr(wt), _ptr(work), _ptr(eids), _ptr(xoff), _ptr(nr),
+                                         _ptr(rows), _ptr(rw), len(eids), len(rows), _ptr(counts),
+                                         _stream(stream)), "mvllm_hip_moe_route_dev")
 
 
 def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):

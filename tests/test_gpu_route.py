@@ -169,3 +169,29 @@ def test_segments_caps_and_bad_ids(hip, orc):
     bad = idx.copy()
     bad[7, 2] = E
     assert gpu_segments(hip, bad, wt, E, E, T * topk)[0] == -1
+
+
+@pytest.mark.parametrize("T,E,k", [(16, 64, 8), (1, 384, 8), (512, 384, 8), (2048, 384, 8),
+                                   (40, 1024, 64), (30, 2000, 3)])
+def test_route_dev(hip, orc, T, E, k):
+    """mvllm_hip_moe_route_dev (top-k and segments in one call) against the oracle's
+    moe_topk per token and moe_segments of its picks."""
+    rng = np.random.default_rng(T * 13 + E + k)
+    choice = (np.round(rng.standard_normal((T, E)) * 8) / 8).astype(np.float32)
+    mix = rng.standard_normal((T, E)).astype(np.float32) if k != 3 else None
+    i32 = dict(dtype=torch.int32, device="cuda")
+    idx, wt = torch.full((T, k), -7, **i32), torch.zeros((T, k), dtype=torch.float32, device="cuda")
+    work, counts = torch.zeros(2 * E + 1, **i32), torch.full((2,), -9, **i32)
+    eids, xoff, nr = (torch.full((E,), -7, **i32) for _ in range(3))
+    rows, rw = torch.full((T * k,), -7, **i32), torch.zeros(T * k, dtype=torch.float32, device="cuda")
+    hip.moe_route_dev(dev(choice), None if mix is None else dev(mix), T, E, k, idx, wt, work,
+                      eids, xoff, nr, rows, rw, counts)
+    torch.cuda.synchronize()
+    gi, gw = idx.cpu().numpy(), wt.cpu().numpy()
+    check_topk(orc, choice, mix, k, gi, gw)
+    nb, n = (int(v) for v in counts.cpu().numpy())
+    say("route_dev", T, E, k, "nb", nb, "rows", n)
+    got = (nb, n, (eids.cpu().numpy()[:nb], xoff.cpu().numpy()[:nb], nr.cpu().numpy()[:nb],
+                   rows.cpu().numpy()[:n], rw.cpu().numpy()[:n]))
+    check_segments(orc, gi, gw, got, E)
+
