@@ -195,3 +195,61 @@ def test_route_dev(hip, orc, T, E, k):
                    rows.cpu().numpy()[:n], rw.cpu().numpy()[:n]))
     check_segments(orc, gi, gw, got, E)
 
+
+
+@pytest.mark.parametrize("fmt,D,I,T,E,k", [(4, 512, 256, 16, 64, 8), (7, 1024, 512, 6, 48, 4)])
+def test_route_feeds_moe_block(hip, orc, fmt, D, I, T, E, k):
+    """One layer batched the way a GPU-resident caller would run it: device routing, its
+    segments and the gathered token rows into one mvllm_hip_moe_block_dev call, against
+    the oracle's host chain (moe_topk per token, moe_segments, moe_block)."""
+    from cases import expert_arrays
+    from mvllm_hip import ACT_CLAMP_SWIGLU, ACT_SITU
+    rng = np.random.default_rng(D + T * E)
+    ex = [expert_arrays(rng, fmt, D, I) for _ in range(E)]
+    X = rng.standard_normal((T, D)).astype(np.float32)
+    choice = rng.standard_normal((T, E)).astype(np.float32)
+    mix = (1 / (1 + np.exp(-choice))).astype(np.float32)
+    act, a, b = (ACT_CLAMP_SWIGLU, 7.0, 0.0) if fmt == 4 else (ACT_SITU, 4.0, 25.0)
+    # device: route, then one batched call
+    i32 = dict(dtype=torch.int32, device="cuda")
+    idx, wt = torch.empty((T, k), **i32), torch.empty((T, k), dtype=torch.float32, device="cuda")
+    work, counts = torch.zeros(2 * E + 1, **i32), torch.empty(2, **i32)
+    eids, xoff, nr = (torch.empty(E, **i32) for _ in range(3))
+    rows, rw = torch.empty(T * k, **i32), torch.empty(T * k, dtype=torch.float32, device="cuda")
+    hip.moe_route_dev(dev(choice), dev(mix), T, E, k, idx, wt, work, eids, xoff, nr, rows, rw,
+                      counts)
+    torch.cuda.synchronize()
+    nb, n = (int(v) for v in counts.cpu().numpy())
+    g_eids, g_xoff, g_nr = (x.cpu().numpy()[:nb] for x in (eids, xoff, nr))
+    g_rows, g_rw = rows.cpu().numpy()[:n], rw.cpu().numpy()[:n]
+    keep = []
+
+    def L(key):
+        out = []
+        for e in g_eids:
+            t = dev(ex[e][key])
+            keep.append(t)
+            out.append(t.data_ptr())
+        return out
+    lists = [L(key) for key in ("gp", "up", "dp", "gs", "us", "ds")]
+    xg = dev(X[g_rows])
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    hip.moe_block_dev(nb, D, I, fmt, *lists, xg, g_xoff, g_nr, g_rows, g_rw, out, T, act, a, b)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    # host: the reference chain on the same scores
+    hi = np.zeros((T, k), np.int32)
+    hw = np.zeros((T, k), np.float32)
+    for t in range(T):
+        _, hi[t], hw[t] = orc.moe_topk(choice[t], k, mix[t])
+    enb, e_eids, e_xoff, e_nr, e_rows, e_rw = orc.moe_segments(hi, hw, T, k, E)
+    assert enb == nb and np.array_equal(e_eids, g_eids) and np.array_equal(e_rows, g_rows)
+    exp = np.zeros((T, D), np.float32)
+    sel = [ex[e] for e in e_eids]
+    assert orc.moe_block(enb, D, I, fmt, *[[s[key] for s in sel] for key in
+                                           ("gp", "up", "dp", "gs", "us", "ds")],
+                         X[e_rows], e_xoff, e_nr, e_rows, e_rw, exp, T, act, a, b) == 1
+    import npref
+    err = npref.rel_err(got, exp)
+    say("route -> moe_block", fmt, "nb", nb, "rows", n, "rel_err", err)
+    assert err < 2e-5
