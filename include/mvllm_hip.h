@@ -49,7 +49,9 @@ const char *mvllm_hip_last_error(void);
  * src/gpu/metal_ops.cpp:448-460).  All pointers are caller-owned HOST memory,
  * exactly as in the reference: per expert e, nr[e] rows of xg starting at row
  * xoff[e] go through gate/up -> act -> down, and out[rows[j]] += rw[j] * y[j]
- * in expert order.  act: 0 Silu, 1 ClampSwiGLU(act_a), 2 SiTU(act_a, act_b).
+ * in expert order (always: this entry never uses the unordered atomic combine, so
+ * equal inputs give bit-identical out from run to run).
+ * act: 0 Silu, 1 ClampSwiGLU(act_a), 2 SiTU(act_a, act_b).
  * Validation and skip rules are the reference's (nb<1, D<1, !out, !xg, fmt not in
  * {0,4,7}, !xoff, !nr -> 0; null expert pointers or Iinter<1 consume rows without
  * writing; rows outside [0,S) (S>0) are skipped).  Expert weights that were
@@ -65,6 +67,11 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
  * moe_block itself, src/gpu/metal_ops.hpp:104-108): the six pointer arrays and
  * xoff/nr/rows/rw are HOST arrays; the weights and scales they point to, xg
  * ([rows, D] f32) and out ([S, D] f32, accumulated) are DEVICE pointers.
+ * Summation order of out: decode-shaped calls (every expert <= 16 rows, matrix-core
+ * decode kernels) fold the combine into the down kernel with float atomics by default,
+ * so out's rows are summed in an arbitrary order and may differ in the last bits from
+ * run to run; option "combine_ordered" = 1 applies the reference's expert order
+ * instead.  Every other call uses the reference's order.
  * Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and the
  * call returns without waiting.  Requires S > 0 (out's row count).  Calls are ordered
  * after each other across streams (they share scratch): a call on another stream than
@@ -77,7 +84,7 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
                             const int *nr, const int *rows, const float *rw, float *out, int S,
                             int act, float act_a, float act_b, void *stream);
 
-/* Options (key, value); returns 1 if the key and value are accepted.
+/* Options (key, value), process-wide; returns 1 if the key and value are accepted.
  *   "mode"   how activations enter the bf16 matrix cores (weights are always decoded
  *            exactly; products and sums are f32):
  *            0  default: decode-shaped calls split each f32 activation into 2 bf16 terms
@@ -93,24 +100,17 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
  *            scaled FP4 matrix cores.  Changes the numbers (activation quantization);
  *            weight scale bytes 0 and 255 act as the hardware's 2^-127 and NaN, not the
  *            reference's +0 and +inf.
- *   "combine_ordered" 1 = decode calls also run the separate combine kernel, which
- *            applies out[t] += w * y in the reference's expert order (bit-exact given the
- *            same expert outputs); by default decode folds the combine into the down
- *            kernel with float atomics (same products, any summation order).
+ *   "combine_ordered" 1 = decode calls of mvllm_hip_moe_block_dev also run the separate
+ *            combine kernel, which applies out[t] += w * y in the reference's expert order
+ *            (bit-exact given the same expert outputs); by default they fold the combine
+ *            into the down kernel with float atomics (same products, any summation
+ *            order).  mvllm_hip_moe_block always uses the ordered combine.
  *   "timing" 1 = record per-phase HIP events; read them with mvllm_hip_stats.
  *   "dec_ks" 0 = automatic; 1, 2, 4 or 8 forces the split of K across waves.
  *   "dec_inline" 1 (default) = the decode gate/up launch carries its descriptors in
  *            its kernel arguments (at most 64 items; same results); 0 = it reads them
  *            from the pinned plan slot.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
- *   "fuse"   1 = decode calls with every expert resident run both projections in one
- *            cooperative launch: the down tasks stream their weights while the gate/up
- *            tasks finish and wait on per-expert counters.  0 (default) = two launches,
- *            measured faster (the cooperative launch and the coherent H stores cost more
- *            than the overlap gains).  Same arithmetic either way.
- *   "gemm_persist" 1 = the grouped GEMM's HBM-bound row classes run persistent
- *            workgroups that prefetch the next task's first K step (same sums; slower
- *            than the default one workgroup per task at current register use).
  * Shapes the matrix-core kernels do not take (fmt 0, D or Iinter not a multiple of
  * 256, misaligned pointers) run an exact f32 kernel instead. */
 int mvllm_hip_set_option(const char *key, long long value);
@@ -199,11 +199,14 @@ void *mvllm_hip_resident_ptr(int layer, int eid);
  *  3 H2D bytes (acts/out) 4 D2H bytes            5 promotions
  *  6 resident hits        7 misses (copied in)   8 evictions
  *  9 kernel ms gate/up    10 kernel ms down      11 kernel ms combine
- *  12 kernel ms quantize  13 launches gate/up    14 launches down
- *  15 launches of both decode projections in one (counted in neither 13 nor 14)
- *  16 waits of such a launch that gave up (sticky; 0 in a correct run)
- * Kernel times are filled only with option "timing"=1 (a fused launch counts as
- * gate/up).  Returns the count written (<= n). */
+ *  12 kernel ms preparing GEMM inputs (the grouped GEMM's bf16 planes of x, or the
+ *     MXFP4 quantization of x and of H)
+ *  13 launches gate/up    14 launches down
+ *  15 host ms spent inside the moe_block entry points (plan building, argument
+ *     marshalling and launches; for mvllm_hip_moe_block also the copies and the wait)
+ *  16 reserved (0)
+ * Kernel times are filled only with option "timing"=1.  Returns the count written
+ * (<= n). */
 int mvllm_hip_stats(double *vals, int n);
 void mvllm_hip_stats_reset(void);
 

@@ -87,16 +87,10 @@ struct TaskD {
     int jbase, nrow, col0;
 };
 
-// Persistent over tasks (PERSIST): workgroup b runs tasks b, b + G, b + 2G, ...
-// (G = gridDim.x) as one stream of K steps.  The loads of the first two steps of task i + 1 are issued
-// during the last two steps of task i (its descriptor is fetched a whole task earlier),
-// so a task's prologue latency and epilogue stores overlap the neighbouring task's
-// streaming.  Without PERSIST (the compute-bound row classes, whose registers are full),
-// or with an odd number of K steps, the host launches one task per workgroup.
-// The 32-row class with one term is held to 128 VGPRs (4 waves per SIMD), so two
+// One workgroup per task.  The 32-row class with one term is held to 128 VGPRs (4 waves per SIMD), so two
 // workgroups share a CU: it needs 126-131 VGPRs, and the cap costs at most a few spilled
 // registers.  Measured on c3: 1.60 -> 1.53 ms per call.
-template <int FMT, bool DUAL, int TERMS, int MT, bool PERSIST>
+template <int FMT, bool DUAL, int TERMS, int MT>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
     constexpr int BM = 16 * MT;
@@ -330,18 +324,14 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
 
     // software pipeline: B two steps ahead in registers; A staged into LDS one step
     // ahead from registers loaded PA steps ahead (PA = 1 for the compute-bound 128-row
-    // class, whose registers are full).  Prefetches past a task's last step go to the
-    // next task (or, after the last task, re-read harmless bytes that are never
-    // consumed), so the body has no branches around its loads; the scheduling barriers
-    // keep each step's uses of a register set ahead of the loads that refill it.
-    int task = blockIdx.x;
+    // class, whose registers are full).  Prefetches past the task's last step re-read
+    // harmless bytes that are never consumed, so the body has no branches around its
+    // loads; the scheduling barriers keep each step's uses of a register set ahead of the
+    // loads that refill it.
+    const int task = blockIdx.x;
     if (task >= n_tasks)
         return;
-    TaskD<FMT> cur = make_task(task);
-    bool has_next = PERSIST && task + (int)gridDim.x < n_tasks;
-    TaskD<FMT> nxt = cur;
-    if (PERSIST && has_next)
-        nxt = make_task(task + (int)gridDim.x);
+    const TaskD<FMT> cur = make_task(task);
     GStep<FMT> b0, b1;
     GScale<FMT> sc, sn;  // scales of this pair of steps / of the next pair
     AStage ra0, ra1;
@@ -361,11 +351,10 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         __syncthreads();
     };
     // Even step k: LDS buffer 0, weights b0; stages A(k + 1) into buffer 1.  Prefetches
-    // past the task's last step belong to the next task (PERSIST) or re-read harmless
-    // bytes.
+    // past the task's last step wrap to its first steps (harmless bytes).
     auto step_even = [&] __attribute__((always_inline)) (int k, auto exact) {
         const bool tail = k + 2 >= nk;
-        const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
+        const TaskD<FMT> &pd = cur;
         const int k2 = tail ? k + 2 - nk : k + 2;
         sc = sn;
         if constexpr (PA == 2)
@@ -382,7 +371,7 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // odd step k + 1: LDS buffer 1, weights b1; stages A(k + 2) into buffer 0
     auto step_odd = [&] __attribute__((always_inline)) (int k, auto exact) {
         const bool tail = k + 2 >= nk;
-        const TaskD<FMT> &pd = PERSIST && tail ? nxt : cur;
+        const TaskD<FMT> &pd = cur;
         const int k2 = tail ? k + 2 - nk : k + 2;
         if constexpr (PA == 2)
             load_a(ra1, pd, min(k2 + 1, nk - 1));
@@ -407,30 +396,20 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             step_even(nk - 1, exact);
     };
     prologue();
-    for (;;) {
-        k_loop(std::false_type{});
-        // Rare second pass: some operand of the task needs the exact decode.  The whole
-        // workgroup runs the task again (the A staging is shared); the next task's
-        // prefetches issued by the loop tail are simply issued once more.  (The same loop
-        // with a uniform branch per step instead of this second copy raised the register
-        // count of the common pass.)
-        if (__syncthreads_or((int)exc)) {
-            exc = 0;
+    k_loop(std::false_type{});
+    // Rare second pass: some operand of the task needs the exact decode.  The whole
+    // workgroup runs the task again (the A staging is shared).  (The same loop with a
+    // uniform branch per step instead of this second copy raised the register count of
+    // the common pass.)
+    if (__syncthreads_or((int)exc)) {
+        exc = 0;
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
-            prologue();
-            k_loop(std::true_type{});
-        }
-        epilogue(cur);
-        if (!PERSIST || !has_next)
-            break;
-        task += (int)gridDim.x;
-        cur = nxt;
-        has_next = task + (int)gridDim.x < n_tasks;
-        if (has_next)
-            nxt = make_task(task + (int)gridDim.x);
+        for (int mt = 0; mt < MT; ++mt)
+            acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
+        prologue();
+        k_loop(std::true_type{});
     }
+    epilogue(cur);
 }
 
 // ---- input planes for the GEMM: gather, split into bf16 terms ------------------------
@@ -482,46 +461,22 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
 
 // ---- launchers ----------------------------------------------------------------------
 
-template <int FMT, bool DUAL, int TERMS, int MT, bool PERSIST>
-static hipError_t launch_gemm_p(GemmArgs a, int n_items, hipStream_t st) {
+template <int FMT, bool DUAL, int TERMS, int MT>
+static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
     const size_t lds = gemm_lds_bytes(FMT, TERMS, MT);
-    auto kern = k_gemm<FMT, DUAL, TERMS, MT, PERSIST>;
-    // resident workgroups of this instantiation (queried once per process)
-    static int resident = 0;
-    if (resident == 0) {
+    auto kern = k_gemm<FMT, DUAL, TERMS, MT>;
+    static bool attr = false;  // the dynamic LDS limit, raised once per process
+    if (!attr) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess)
             return e;
-        int dev = 0, cus = 0, per_cu = 0;
-        if ((e = hipGetDevice(&dev)) != hipSuccess ||
-            (e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) !=
-                hipSuccess ||
-            (e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                 &per_cu, reinterpret_cast<const void *>(kern), kGemmThreads, lds)) != hipSuccess)
-            return e;
-        resident = std::max(1, cus * std::max(1, per_cu));
+        attr = true;
     }
     a.n_tasks = n_items * a.nbn;
-    // persistent (cross-task prefetch) only with an even number of K steps
-    const int grid = PERSIST && (a.K / kGemmBK) % 2 == 0 ? std::min(a.n_tasks, resident)
-                                                         : a.n_tasks;
-    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(kGemmThreads), lds, st, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)a.n_tasks), dim3(kGemmThreads), lds, st, a);
     return hipGetLastError();
 }
-
-static bool g_gemm_persist = false;  // measured slower than independent workgroups
-
-template <int FMT, bool DUAL, int TERMS, int MT>
-static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
-    if constexpr (MT <= 2 && !(TERMS == 2 && MT == 2)) {  // (that one spills)
-        if (g_gemm_persist && (a.K / kGemmBK) % 2 == 0)
-            return launch_gemm_p<FMT, DUAL, TERMS, MT, true>(a, n_items, st);
-    }
-    return launch_gemm_p<FMT, DUAL, TERMS, MT, false>(a, n_items, st);
-}
-
-void gemm_set_persistent(bool on) { g_gemm_persist = on; }
 
 template <int FMT, bool DUAL>
 static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int mt,

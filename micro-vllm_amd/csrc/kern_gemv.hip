@@ -35,8 +35,12 @@ __device__ __forceinline__ float dev_act(int act, float g, float u, float a, flo
         if (a > 0.f && g > a)
             g = a;
         const float s = g * dev_sigmoid(g);
-        if (a > 0.f)
-            u = fminf(fmaxf(u, -a), a);
+        if (a > 0.f) {  // comparisons, as the reference: a NaN up stays NaN
+            if (u > a)
+                u = a;
+            if (u < -a)
+                u = -a;
+        }
         return s * u;
     }
     if (act == ACT_SITU)  // src/quant/quant.hpp:32-34

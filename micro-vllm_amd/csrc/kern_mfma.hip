@@ -15,8 +15,8 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4))
 void k_mfma_dec(DecArgs A) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int item = blockIdx.x / A.wgs;
-    dec_task<FMT, DUAL, TERMS, KS, NT, SR, false, PACK>(A, item, blockIdx.x - item * A.wgs,
-                                                        (int)threadIdx.x, smem, DecSync{});
+    dec_task<FMT, DUAL, TERMS, KS, NT, SR, PACK>(A, item, blockIdx.x - item * A.wgs,
+                                                 (int)threadIdx.x, smem);
 }
 
 // Gate/up with its descriptors in the kernel arguments (device memory at launch).
@@ -25,8 +25,8 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4))
 void k_mfma_dec_inl(DecArgs A, DecInline I) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int item = blockIdx.x / A.wgs;
-    dec_task<FMT, true, TERMS, KS, 2, SR, false, PACK, true>(
-        A, item, blockIdx.x - item * A.wgs, (int)threadIdx.x, smem, DecSync{}, I.d);
+    dec_task<FMT, true, TERMS, KS, 2, SR, PACK, true>(A, item, blockIdx.x - item * A.wgs,
+                                                      (int)threadIdx.x, smem, I.d);
 }
 
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt) {

@@ -27,8 +27,12 @@ __device__ __forceinline__ float mf_act(int act, float g, float u, float a, floa
         if (a > 0.f && g > a)
             g = a;
         const float s = g * mf_sigmoid(g);
-        if (a > 0.f)
-            u = fminf(fmaxf(u, -a), a);
+        if (a > 0.f) {  // comparisons, as the reference: a NaN up stays NaN
+            if (u > a)
+                u = a;
+            if (u < -a)
+                u = -a;
+        }
         return s * u;
     }
     if (act == ACT_SITU)

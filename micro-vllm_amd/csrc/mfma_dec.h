@@ -1,5 +1,4 @@
-// mfma_dec.h -- the decode-shaped matrix-core task shared by the two-launch decode
-// kernels (kern_mfma.hip) and the fused single launch (kern_fused.hip).
+// mfma_dec.h -- the decode-shaped matrix-core task of the decode kernels (kern_mfma.hip).
 //
 // Both moe_block projections, H = act(X Wg^T, X Wu^T) and Y = H Wd^T, run as
 // C[token, o] = sum_k A[token, k] * B[k, o] with A = activations (16 tokens per tile),
@@ -295,20 +294,6 @@ __host__ __device__ inline size_t dec_lds_plan(int fmt, int K, int rmax, int ter
     return tot + 128;
 }
 
-// Cross-workgroup hooks of the fused launch (k_mfma_fused).  The per-XCD L2s are not
-// coherent with each other inside a kernel, so H and its partial sums travel with
-// agent-scope (sc1) stores and loads, which the L2s do not keep stale: a gate/up task
-// stores them so, waits until every wave's stores are complete, then adds 1 to
-// done[slot]; a down task issues its first weight loads, waits until done[slot] reaches
-// its target, then reads them so.  No L2 write-back or invalidation is needed.  The
-// counters only grow; the host keeps each slot's running target.
-struct DecSync {
-    unsigned *done;  // per expert slot
-    int *err;        // set when a wait gives up
-};
-
-constexpr int kSpinLimit = 1 << 20;  // ~1 s of polling; a wait never outlives this
-
 // A pointer every lane holds the same value of, made visibly uniform (SGPRs): a buffer
 // resource the compiler cannot prove uniform makes each load a loop over the lanes.
 __device__ __forceinline__ const void *uniform_ptr(const void *p) {
@@ -318,13 +303,12 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
     return reinterpret_cast<const void *>(((unsigned long long)hi << 32) | lo);
 }
 
-// One task: item `item`, column block `wg` of one projection.  FUSED adds the hooks.
+// One task: item `item`, column block `wg` of one projection.
 // INL: the descriptor comes from `kd` (compact, in the kernel arguments), not A.desc.
-template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool FUSED, bool PACK = false,
+template <int FMT, bool DUAL, int TERMS, int KS, int NT, int SR, bool PACK = false,
           bool INL = false>
 __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int tid,
-                                         char *smem, const DecSync &sy,
-                                         const DecDescK *kd = nullptr) {
+                                         char *smem, const DecDescK *kd = nullptr) {
     constexpr int TW = kDecWaves / KS;   // wave slots per K range
     constexpr int NU = NT == 2 ? 2 : 4;  // K blocks per tile in flight (VGPR budget)
     constexpr int XSR = 2;               // single, fmt 4: sums per thread (K / 4 <= 2048)
@@ -337,11 +321,11 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
     // below: vector loads complete in order, so nothing waits for it early.
     const int cpi = item * A.wgs + wg;
     const bool cp =
-        DUAL && !FUSED && cpi < A.n_cp && __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
+        DUAL && cpi < A.n_cp && __builtin_amdgcn_readfirstlane(tid >> 6) == 0;
     u32x4 cpv = {0u, 0u, 0u, 0u};
     if (cp)
         cpv = reinterpret_cast<const u32x4 *>(A.cp_src + cpi)[tid & 15];
-    static_assert(!INL || (DUAL && !FUSED), "compact descriptors are gate/up only");
+    static_assert(!INL || DUAL, "compact descriptors are gate/up only");
     const DecDesc &dd = A.desc[INL ? 0 : item];  // not read when INL
     const int K = A.K, O = A.O;
     const void *wp[2], *sp[2];
@@ -440,15 +424,7 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
             const int tm = row / nrow, r = row - tm * nrow;
             const u32x4 *src = reinterpret_cast<const u32x4 *>(
                                    A.pin + ((size_t)tm * A.rcap + jbase + r) * (size_t)K) + c;
-            if constexpr (FUSED) {  // written by other workgroups in this launch
-                const unsigned *sw = reinterpret_cast<const unsigned *>(src);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    st[u][e] = __hip_atomic_load(sw + e, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-            } else {
-                st[u] = *src;
-            }
+            st[u] = *src;
         }
         if constexpr (FMT == 4) {
 #pragma unroll
@@ -460,13 +436,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                     A.xs + (size_t)(ok ? g : 0) * 4 * A.rcap + jbase + (ok ? r : 0);
                 float p4[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if constexpr (FUSED)
-                        p4[e] = __hip_atomic_load(pp + e * A.rcap, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                    else
-                        p4[e] = pp[e * A.rcap];
-                }
+                for (int e = 0; e < 4; ++e)
+                    p4[e] = pp[e * A.rcap];
                 xsr[u] = ok ? ((p4[0] + p4[1]) + p4[2]) + p4[3] : 0.f;
             }
         }
@@ -488,27 +459,8 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
             for (int n = 0; n < NT; ++n)
                 load_dblock<FMT>(b[u][n], rw[n], vw[n], kw0 + 256 * (u < nblk ? u : nblk - 1));
     };
-    if constexpr (FUSED && !DUAL) {
-        // the weights do not depend on H: stream them while the gate/up tasks finish
-        prefetch();
-        if (tid == 0) {
-            const unsigned target = (unsigned)dd.pad0[1];
-            int n = 0;
-            while ((int)(__hip_atomic_load(sy.done + dd.pad0[0], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT) - target) < 0) {
-                __builtin_amdgcn_s_sleep(2);
-                if (++n > kSpinLimit) {
-                    __hip_atomic_store(sy.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
-            }
-        }
-        __syncthreads();  // H reads below come after thread 0's acquire
-        stage_loads();
-    } else {
-        stage_loads();
-        prefetch();
-    }
+    stage_loads();
+    prefetch();
     // every load above stays above (the compiler would otherwise sink the staging loads
     // into the stores' branches, behind a full wait); emits no instruction
     asm volatile("" ::: "memory");
@@ -699,28 +651,16 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
             if (tok < nrow) {
                 const int pos = (o & ~7) + a_slot<FMT>(o & 7);
 #pragma unroll
-                for (int tm = 0; tm < TERMS; ++tm) {
-                    __bf16 *dst = A.pout + ((size_t)tm * A.rcap + j) * O + pos;
-                    if constexpr (FUSED)  // read by other workgroups in this launch
-                        __hip_atomic_store(reinterpret_cast<unsigned short *>(dst),
-                                           __builtin_bit_cast(unsigned short, tt[tm]),
-                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    else
-                        *dst = tt[tm];
-                }
+                for (int tm = 0; tm < TERMS; ++tm)
+                    A.pout[((size_t)tm * A.rcap + j) * O + pos] = tt[tm];
             }
             if constexpr (FMT == 4) {
                 rep += __shfl_xor(rep, 1, 16);
                 rep += __shfl_xor(rep, 2, 16);
                 rep += __shfl_xor(rep, 4, 16);
                 rep += __shfl_xor(rep, 8, 16);
-                if (t == 0 && tok < nrow) {
-                    float *dst = A.hp + ((size_t)(tl >> 2) * 4 + (tl & 3)) * A.rcap + j;
-                    if constexpr (FUSED)
-                        __hip_atomic_store(dst, rep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    else
-                        *dst = rep;
-                }
+                if (t == 0 && tok < nrow)
+                    A.hp[((size_t)(tl >> 2) * 4 + (tl & 3)) * A.rcap + j] = rep;
             }
         }
     } else {
@@ -748,14 +688,6 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
                 }
             }
         }
-    }
-    if constexpr (FUSED && DUAL) {
-        // publish H: every wave's (agent-scope) stores complete, then the count
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0)
-            __hip_atomic_fetch_add(sy.done + dd.pad0[0], 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

@@ -139,23 +139,6 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
                            const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
                            const DecDescK *inl = nullptr);
 
-// Both decode projections in one cooperative launch (kern_fused.hip), the down projection
-// folding the combine into out.  Descriptors as for launch_mfma_dec, plus: pad0[0] =
-// expert slot (index of the expert's counter in done) in both phases; down pad0[1] =
-// the value done[slot] reaches once this call's gate/up tasks of the expert are stored
-// (the counters only grow: the caller keeps each slot's running total and adds, per
-// call, the gate/up items of the slot x I / (16 * kDecWaves / ks_gu)).  err is set if a
-// wait gave up (never in a correct run).  Terms 2 only; the kernel variants cover
-// ks_gu in {1, 2, 4, 8}, (ks_dn, nt_dn) in {(1, 2), (1, 1), (2, 1), (4, 1)} and down items
-// of 2 * rmax_dn * I / 8 <= 4 * kDecThreads staged chunks.
-bool fused_supported(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn, int rmax_dn, int I);
-hipError_t launch_mfma_fused(int fmt, int terms, int ks_gu, int ks_dn, int nt_dn,
-                             const DecDesc *gu_desc, int n_gu_items, const DecDesc *dn_desc,
-                             int n_dn_items, const float *xin, void *planes, float *hp,
-                             float *out, int D, int I, int rcap, int rmax_gu, int rmax_dn,
-                             int act, float act_a, float act_b, unsigned *done, int *err,
-                             hipStream_t st);
-
 // Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
 // nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per
 // (item, block of 128 columns of each of gate/up, or 256 columns of down).  Requires
@@ -172,10 +155,6 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act, float act_a, float act_b,
                        hipStream_t st);
-// Option "gemm_persist": the HBM-bound row classes (mt <= 2) run persistent workgroups that
-// prefetch across tasks.  Off by default: on c3/c4 it measured 5-6% slower than launching
-// one workgroup per task (several per CU overlap each other's prologues and tails).
-void gemm_set_persistent(bool on);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
                               int K, int rcap, void *planes, hipStream_t st);
 

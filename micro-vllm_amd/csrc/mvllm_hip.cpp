@@ -60,7 +60,13 @@ void set_err(const std::string &s) { g_err = s; }
         }                                                                                     \
     } while (0)
 
-// grow-only device buffer; growing waits for the device so no in-flight kernel reads it
+// Buffers a grow-only device buffer has outgrown.  Work already enqueued may still read
+// them, so they are not freed when replaced (a free would have to drain the device first,
+// in the middle of a call); they are kept until shutdown.  Growth is geometric, so what is
+// kept stays below the live buffers' own size.
+std::vector<void *> g_retired;
+
+// grow-only device buffer
 struct DevBuf {
     void *p = nullptr;
     size_t cap = 0;
@@ -69,18 +75,15 @@ struct DevBuf {
             return hipSuccess;
         size_t want = std::max(bytes, cap + cap / 2);
         want = (want + 255) & ~size_t(255);
-        if (p) {
-            hipError_t e = hipDeviceSynchronize();
-            if (e != hipSuccess)
-                return e;
-            (void)hipFree(p);
-            p = nullptr;
-            cap = 0;
-        }
-        hipError_t e = hipMalloc(&p, want);
-        if (e == hipSuccess)
-            cap = want;
-        return e;
+        void *np = nullptr;
+        hipError_t e = hipMalloc(&np, want);
+        if (e != hipSuccess)
+            return e;
+        if (p)
+            g_retired.push_back(p);
+        p = np;
+        cap = want;
+        return hipSuccess;
     }
     void release() {
         if (p)
@@ -133,8 +136,12 @@ struct Resident {
     std::list<long long>::iterator lru;
 };
 
+// Per-phase events of one call: start, after the input preparation (bf16 planes or MXFP4
+// quantization of x), after the gate/up kernels, after the preparation of H (MXFP4
+// quantization), after the down kernels, after the combine.  Phases a path does not have
+// are empty spans.
 struct TimedCall {
-    hipEvent_t ev[4];  // start, after gate/up, after down, after combine
+    hipEvent_t ev[6];
 };
 
 struct Ctx {
@@ -148,6 +155,7 @@ struct Ctx {
     // previous call's stream when such a call comes, not after every call.  Every event
     // recorded is a queue packet that idles the GPU between two calls' kernels (~4.6 us).
     hipEvent_t prev_done = nullptr;
+    hipEvent_t miss_done = nullptr;  // the staged path's miss copies (copy stream)
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     HostBuf hx, ho;
@@ -167,13 +175,7 @@ struct Ctx {
     int gemm = 0;            // grouped GEMM: 0 auto, 1 whenever it applies, 2 never
     int fp4act = 0;          // MXFP4 experts: 1 = quantize activations, native FP4 GEMMs
     int combine_ordered = 0;  // 1 = separate combine in the reference's order (decode too)
-    int fuse = 0;            // decode: both projections in one cooperative launch
     int dec_inline = 1;      // decode: gate/up descriptors in the kernel arguments when they fit
-    // fused launch: per expert slot, gate/up tasks finished on the device (only grows) and
-    // the host's running total of what was launched; err[0] = a wait gave up
-    DevBuf sync;             // [16] int err + unsigned done[cap]
-    size_t sync_cap = 0;
-    std::vector<unsigned> cum, adds;
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
@@ -191,6 +193,17 @@ Ctx &ctx() {
     static Ctx c;
     return c;
 }
+
+// Host time spent inside an entry point, added to stats[15] (ms) when the scope ends.
+struct HostClock {
+    double *acc;
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    explicit HostClock(double *a) : acc(a) {}
+    ~HostClock() {
+        *acc += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0)
+                    .count();
+    }
+};
 
 long long res_key(int layer, int eid) {
     return (static_cast<long long>(layer) << 32) | static_cast<unsigned>(eid);
@@ -305,7 +318,6 @@ struct CallCfg {
     bool gemm = false;        // grouped GEMM (prefill-shaped)
     bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
     bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
-    bool fused = false;       // decode kernels: one cooperative launch for both projections
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
@@ -431,8 +443,10 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     cc.gemm = true;
 }
 
+// ordered: the combine keeps the reference's expert order even for decode-shaped calls
+// (no float-atomic fold into the down kernel).
 void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, size_t split,
-               const void *in) {
+               const void *in, bool ordered) {
     cc = CallCfg();
     // bf16 terms per activation: 2 (default) represents each f32 activation to 2^-17
     // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2).  The grouped GEMM takes
@@ -468,12 +482,8 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
                   add_phase(C, cc, cc.dn, P, P.ew.size(), fmt, I, D, false);
         if (cc.mfma) {
             // decode-sized outputs: fold the combine into the down kernel (one launch less);
-            // option combine_ordered keeps the reference's summation order instead
-            cc.atomic_combine = !C.combine_ordered;
-            // both projections in one launch when every expert is resident at launch time
-            cc.fused = C.fuse && cc.atomic_combine && split >= P.ew.size() &&
-                       fused_supported(fmt, cc.terms, cc.gu.ks, cc.dn.ks, cc.dn.nt,
-                                       cc.dn.rmax, I);
+            // an ordered call keeps the reference's summation order instead
+            cc.atomic_combine = !ordered;
             return;
         }
         cc.items.clear();
@@ -482,6 +492,54 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
         cc.terms = C.mode == 2 ? 1 : 2;  // the decode accuracy (2 terms) unless mode 2
         plan_gemm(cc, P, split, fmt);
     }
+}
+
+// Device scratch of one call: the exact path's f32 H; the matrix-core paths' H planes
+// Ph (+ int4 partial sums HP); the down output Y (not written when the decode kernels fold
+// the combine into out); the grouped GEMM's input planes (or MXFP4 codes) Xp.
+struct Bufs {
+    void *H = nullptr, *Y = nullptr, *Ph = nullptr, *HP = nullptr, *Xp = nullptr;
+};
+
+// Bytes of each buffer of Bufs that a call of R compact rows uses (0 = unused).
+void buf_sizes(const CallCfg &cc, size_t R, int D, int I, size_t sz[5]) {
+    const size_t tb = (size_t)cc.terms * 2;
+    for (int i = 0; i < 5; ++i)
+        sz[i] = 0;
+    if (cc.fp4) {
+        sz[0] = R * I * 4;
+        sz[1] = R * D * 4;
+        sz[2] = R * (I / 2 + I / 32);
+        sz[4] = R * (D / 2 + D / 32);
+    } else if (cc.gemm) {
+        sz[1] = R * D * 4;
+        sz[2] = tb * R * I;
+        sz[4] = tb * R * D;
+    } else if (cc.mfma) {
+        sz[1] = cc.atomic_combine ? 0 : R * D * 4;
+        sz[2] = tb * R * I;
+        sz[3] = (size_t)(I / 64) * 4 * R * 4;
+    } else {
+        sz[0] = R * I * 4;
+        sz[1] = R * D * 4;
+    }
+}
+
+// The call's buffers from the library's grow-only device buffers.
+hipError_t get_bufs(Ctx &C, const CallCfg &cc, size_t R, int D, int I, Bufs &B) {
+    size_t sz[5];
+    buf_sizes(cc, R, D, I, sz);
+    DevBuf *db[5] = {&C.H, &C.Y, &C.Ph, &C.HP, &C.Xp};
+    void **dst[5] = {&B.H, &B.Y, &B.Ph, &B.HP, &B.Xp};
+    for (int i = 0; i < 5; ++i) {
+        if (!sz[i])
+            continue;
+        hipError_t e = db[i]->ensure(sz[i]);
+        if (e != hipSuccess)
+            return e;
+        *dst[i] = db[i]->p;
+    }
+    return hipSuccess;
 }
 
 // Upload the plan (experts, xrow, combine CSR, items) through a pinned slot; returns
@@ -583,6 +641,7 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw + b_dg + b_dd;
     HIP_TRY(s.host.ensure(total));
     HIP_TRY(s.dev.ensure(total));
+    char *dbase = static_cast<char *>(s.dev.p);
     char *h = static_cast<char *>(s.host.p);
     size_t o = 0;
     auto put = [&](const void *src, size_t n, size_t b) {
@@ -608,36 +667,11 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     o += b_rd;
     const size_t o_rw = put(P.w.data(), R * 4, b_rw);
     const size_t o_dg = o, o_dd = o + b_dg;
-    if (cc.fused) {
-        const size_t ne = P.ew.size();
-        if (ne > C.sync_cap) {  // grow: the device counters restart from zero
-            const size_t cap = std::max<size_t>(ne, 256);
-            HIP_TRY(C.sync.ensure(64 + cap * 4));
-            HIP_TRY(hipMemset(C.sync.p, 0, 64 + cap * 4));
-            C.sync_cap = cap;
-            C.cum.assign(cap, 0u);
-        }
-        C.adds.assign(ne, 0u);
-        const unsigned gwgs = (unsigned)(P.I / (16 * (kDecWaves / cc.gu.ks)));
-        for (size_t it = cc.gu.it0; it < cc.gu.it1; ++it)
-            C.adds[cc.items[4 * it]] += gwgs;
-    }
     if (cc.mfma) {
         build_desc(P, cc, cc.gu.it0, cc.gu.it1, true, rows_identity, rdest,
                    reinterpret_cast<DecDesc *>(h + o_dg));
         build_desc(P, cc, cc.dn.it0, cc.dn.it1, false, rows_identity, rdest,
                    reinterpret_cast<DecDesc *>(h + o_dd));
-        if (cc.fused) {  // expert slots, and the counts the down tasks wait for
-            DecDesc *g = reinterpret_cast<DecDesc *>(h + o_dg);
-            for (size_t it = cc.gu.it0; it < cc.gu.it1; ++it)
-                g[it - cc.gu.it0].pad0[0] = cc.items[4 * it];
-            DecDesc *d = reinterpret_cast<DecDesc *>(h + o_dd);
-            for (size_t it = cc.dn.it0; it < cc.dn.it1; ++it) {
-                const int slot = cc.items[4 * it];
-                d[it - cc.dn.it0].pad0[0] = slot;
-                d[it - cc.dn.it0].pad0[1] = (int)(C.cum[slot] + C.adds[slot]);
-            }
-        }
     }
     o += b_dg + b_dd;
     // The decode kernels with the folded combine read nothing of the plan but their
@@ -646,8 +680,8 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const bool zero_copy = cc.mfma && cc.atomic_combine;
     char *d = static_cast<char *>(s.host.p);
     if (!zero_copy) {
-        HIP_TRY(hipMemcpyAsync(s.dev.p, s.host.p, total, hipMemcpyHostToDevice, st));
-        d = static_cast<char *>(s.dev.p);
+        HIP_TRY(hipMemcpyAsync(dbase, s.host.p, total, hipMemcpyHostToDevice, st));
+        d = dbase;
     }
     dp.ew = reinterpret_cast<ExpertWork *>(d + o_ew);
     dp.xrow = reinterpret_cast<int *>(d + o_x);
@@ -661,7 +695,7 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.gu_desc = reinterpret_cast<DecDesc *>(d + o_dg);
     dp.gu_host = reinterpret_cast<const DecDesc *>(h + o_dg);
     dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
-    dp.dn_desc_dev = reinterpret_cast<DecDesc *>(static_cast<char *>(s.dev.p) + o_dd);
+    dp.dn_desc_dev = reinterpret_cast<DecDesc *>(dbase + o_dd);
     if (!zero_copy)
         dp.dn_desc_dev = dp.dn_desc;  // already there
     dp.slot = si;
@@ -719,27 +753,30 @@ GemvArgs generic_args(const DevPlan &dp, size_t first, size_t count, const int *
 
 // The phases of one call.  Experts [0, split) run gate/up first; a wait on `gate_event`
 // (may be null) precedes gate/up of [split, n).
-int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int fmt, int D,
-               int I, int act, float a, float b, const float *in, const int *in_rows, float *out,
-               hipStream_t st, size_t split, hipEvent_t gate_event) {
+int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, const Bufs &B,
+               int fmt, int D, int I, int act, float a, float b, const float *in,
+               const int *in_rows, float *out, hipStream_t st, size_t split,
+               hipEvent_t gate_event) {
+    const bool timing = C.timing != 0;  // per-phase events (created per call)
     const size_t n = P.ew.size(), R = P.xrow.size();
     const int rcap = static_cast<int>(R);
     TimedCall tc{};
-    if (C.timing) {
+    if (timing) {
         // no system-scope release: its L2 write-back would sit inside the timed spans
         for (auto &e : tc.ev)
             HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
-        HIP_TRY(hipEventRecord(tc.ev[0], st));
     }
+    // records the event that ends phase i (TimedCall), when timing
+    auto mark = [&](int i) { return timing ? hipEventRecord(tc.ev[i], st) : hipSuccess; };
+    HIP_TRY(mark(0));
     if (cc.fp4) {
         // activations quantized to MXFP4 (bit-exact with fp4_activation_qdq), the gate/up
         // GEMM writes H f32, H is quantized, the down GEMM writes Y
-        HIP_TRY(C.Xp.ensure(std::max<size_t>(R * (D / 2 + D / 32), 256)));
-        HIP_TRY(C.Ph.ensure(std::max<size_t>(R * (I / 2 + I / 32), 256)));
-        uint8_t *xq = static_cast<uint8_t *>(C.Xp.p), *xsc = xq + R * (D / 2);
-        uint8_t *hq = static_cast<uint8_t *>(C.Ph.p), *hsc = hq + R * (I / 2);
-        float *H = static_cast<float *>(C.H.p);
+        uint8_t *xq = static_cast<uint8_t *>(B.Xp), *xsc = xq + R * (D / 2);
+        uint8_t *hq = static_cast<uint8_t *>(B.Ph), *hsc = hq + R * (I / 2);
+        float *H = static_cast<float *>(B.H);
         HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows));
+        HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             if (part == 1 && gate_event)
                 HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
@@ -754,21 +791,19 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 C.stats[13] += 1;
             }
         }
+        HIP_TRY(mark(2));
         HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st));
-        if (C.timing)
-            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(mark(3));
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
             HIP_TRY(launch_gemm_fp4(false, g.mt, dp.ew, dp.items + 4 * g.it0,
                                     static_cast<int>(g.it1 - g.it0), hq, hsc, nullptr,
-                                    static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
+                                    static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f, st));
             C.stats[14] += 1;
         }
     } else if (cc.gemm) {
-        const size_t tb = (size_t)cc.terms * 2;
-        HIP_TRY(C.Xp.ensure(std::max<size_t>(tb * R * D, 256)));
-        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
-        HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, C.Xp.p, st));
+        HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, B.Xp, st));
+        HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             if (part == 1 && gate_event)
                 HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
@@ -778,40 +813,21 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 if (i1 <= i0)
                     continue;
                 HIP_TRY(launch_gemm(fmt, true, cc.terms, g.mt, dp.ew, dp.items + 4 * i0,
-                                    static_cast<int>(i1 - i0), C.Xp.p, C.Ph.p, nullptr, D, I,
+                                    static_cast<int>(i1 - i0), B.Xp, B.Ph, nullptr, D, I,
                                     rcap, act, a, b, st));
                 C.stats[13] += 1;
             }
         }
-        if (C.timing)
-            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(mark(2));
+        HIP_TRY(mark(3));
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
             HIP_TRY(launch_gemm(fmt, false, cc.terms, g.mt, dp.ew, dp.items + 4 * g.it0,
-                                static_cast<int>(g.it1 - g.it0), C.Ph.p, nullptr,
-                                static_cast<float *>(C.Y.p), I, D, rcap, 0, 0.f, 0.f, st));
+                                static_cast<int>(g.it1 - g.it0), B.Ph, nullptr,
+                                static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f, st));
             C.stats[14] += 1;
         }
-    } else if (cc.fused) {
-        const size_t tb = (size_t)cc.terms * 2;
-        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
-        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
-        char *sy = static_cast<char *>(C.sync.p);
-        HIP_TRY(launch_mfma_fused(fmt, cc.terms, cc.gu.ks, cc.dn.ks, cc.dn.nt, dp.gu_desc,
-                                  static_cast<int>(cc.gu.it1 - cc.gu.it0), dp.dn_desc,
-                                  static_cast<int>(cc.dn.it1 - cc.dn.it0), in, C.Ph.p,
-                                  static_cast<float *>(C.HP.p), out, D, I, rcap, cc.gu.rmax,
-                                  cc.dn.rmax, act, a, b, reinterpret_cast<unsigned *>(sy + 64),
-                                  reinterpret_cast<int *>(sy), st));
-        for (size_t e = 0; e < C.adds.size(); ++e)  // launched: the targets move on
-            C.cum[e] += C.adds[e];
-        C.stats[15] += 1;
-        if (C.timing)
-            HIP_TRY(hipEventRecord(tc.ev[1], st));
     } else if (cc.mfma) {
-        const size_t tb = (size_t)cc.terms * 2;
-        HIP_TRY(C.Ph.ensure(std::max<size_t>(tb * R * I, 256)));
-        HIP_TRY(C.HP.ensure(std::max<size_t>((size_t)(I / 64) * 4 * R * 4, 256)));
         // the gate/up workgroups copy the down descriptors from the pinned plan slot to
         // device memory (when they are not there already), a descriptor a workgroup
         const int n_dn = static_cast<int>(cc.dn.it1 - cc.dn.it0);
@@ -828,6 +844,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
         const bool pk_gu = cc.terms == 2 && mr_gu <= 8, pk_dn = cc.terms == 2 && mr_dn <= 8;
         const int rmax_gu = pk_gu ? mr_gu : cc.gu.rmax, rmax_dn = pk_dn ? mr_dn : cc.dn.rmax;
         int copied = dp.dn_desc_dev == dp.dn_desc ? n_dn : 0;
+        HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             const size_t i0 = part ? cc.gu.it_split : cc.gu.it0;
             const size_t i1 = part ? cc.gu.it1 : cc.gu.it_split;
@@ -841,7 +858,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             const bool inl = C.dec_inline && compact_desc(dp.gu_host + (i0 - cc.gu.it0), ni, kd);
             HIP_TRY(launch_mfma_dec(fmt, true, cc.terms, cc.gu.ks, cc.gu.nt,
                                     dp.gu_desc + (i0 - cc.gu.it0), ni, in, nullptr, nullptr,
-                                    C.Ph.p, static_cast<float *>(C.HP.p), nullptr, D, I, rcap,
+                                    B.Ph, static_cast<float *>(B.HP), nullptr, D, I, rcap,
                                     rmax_gu, act, a, b, false, pk_gu, dp.dn_desc + copied,
                                     dp.dn_desc_dev + copied, ncp, st, inl ? kd : nullptr));
             copied += ncp;
@@ -851,16 +868,17 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
             HIP_TRY(hipMemcpyAsync(dp.dn_desc_dev + copied, dp.dn_desc + copied,
                                    (size_t)(n_dn - copied) * sizeof(DecDesc),
                                    hipMemcpyHostToDevice, st));
-        if (C.timing)
-            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(mark(2));
+        HIP_TRY(mark(3));
         HIP_TRY(launch_mfma_dec(fmt, false, cc.terms, cc.dn.ks, cc.dn.nt, dp.dn_desc_dev,
-                                static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, C.Ph.p,
-                                static_cast<const float *>(C.HP.p), nullptr, nullptr,
-                                cc.atomic_combine ? out : static_cast<float *>(C.Y.p), I, D,
+                                static_cast<int>(cc.dn.it1 - cc.dn.it0), nullptr, B.Ph,
+                                static_cast<const float *>(B.HP), nullptr, nullptr,
+                                cc.atomic_combine ? out : static_cast<float *>(B.Y), I, D,
                                 rcap, rmax_dn, 0, 0.f, 0.f, cc.atomic_combine, pk_dn, nullptr,
                                 nullptr, 0, st));
         C.stats[14] += 1;
     } else {
+        HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             const size_t first = part == 0 ? 0 : split, cnt = part == 0 ? split : n - split;
             if (part == 1 && gate_event)
@@ -869,31 +887,30 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
                 continue;
             HIP_TRY(launch_gemv_generic(fmt, true,
                                         generic_args(dp, first, cnt, in_rows, in,
-                                                     static_cast<float *>(C.H.p), D, I, act, a, b),
+                                                     static_cast<float *>(B.H), D, I, act, a, b),
                                         st));
             C.stats[13] += 1;
         }
-        if (C.timing)
-            HIP_TRY(hipEventRecord(tc.ev[1], st));
+        HIP_TRY(mark(2));
+        HIP_TRY(mark(3));
         HIP_TRY(launch_gemv_generic(fmt, false,
                                     generic_args(dp, 0, n, nullptr,
-                                                 static_cast<const float *>(C.H.p),
-                                                 static_cast<float *>(C.Y.p), I, D, 0, 0.f, 0.f),
+                                                 static_cast<const float *>(B.H),
+                                                 static_cast<float *>(B.Y), I, D, 0, 0.f, 0.f),
                                     st));
         C.stats[14] += 1;
     }
-    if (C.timing)
-        HIP_TRY(hipEventRecord(tc.ev[2], st));
+    HIP_TRY(mark(4));
     if (cc.atomic_combine) {  // already folded into the down kernel
-        if (C.timing) {
-            HIP_TRY(hipEventRecord(tc.ev[3], st));
+        if (timing) {
+            HIP_TRY(mark(5));
             C.timed.push_back(tc);
         }
         C.stats[1] += static_cast<double>(R);
         return 1;
     }
     CombineArgs cb{};
-    cb.Y = static_cast<const float *>(C.Y.p);
+    cb.Y = static_cast<const float *>(B.Y);
     cb.tok_ptr = dp.tok_ptr;
     cb.ent_row = dp.ent_row;
     cb.ent_w = dp.ent_w;
@@ -902,12 +919,40 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, int 
     cb.n_tok = static_cast<int>(P.out_row.size());
     cb.D = D;
     HIP_TRY(launch_combine(cb, st));
-    if (C.timing) {
-        HIP_TRY(hipEventRecord(tc.ev[3], st));
+    if (timing) {
+        HIP_TRY(mark(5));
         C.timed.push_back(tc);
     }
     C.stats[1] += static_cast<double>(R);
     return 1;
+}
+
+// One mvllm_hip_moe_block_dev call (arguments validated).
+int dev_call(Ctx &C, int nb, int D, int Iinter, int fmt, const void *const *g,
+             const void *const *u, const void *const *d, const float *const *gs,
+             const float *const *us, const float *const *ds, const float *xg, const int *xoff,
+             const int *nr, const int *rows, const float *rw, float *out, int S, int act,
+             float act_a, float act_b, hipStream_t st) {
+    HostClock hc(&C.stats[15]);
+    Plan P;
+    build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
+    C.stats[0] += 1;
+    if (P.ew.empty())
+        return 1;
+    const size_t R = P.xrow.size();
+    CallCfg cc;
+    plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg, C.combine_ordered != 0);
+    Bufs B;
+    if (!order_after_previous(C, st))
+        return 0;
+    HIP_TRY(get_bufs(C, cc, R, D, Iinter, B));
+    DevPlan dp{};
+    if (!upload_plan(C, P, cc, st, dp, false))
+        return 0;
+    if (!run_phases(C, P, cc, dp, B, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
+                    P.ew.size(), nullptr))
+        return 0;
+    return finish_call(C, st, dp.slot);
 }
 
 bool args_ok(int nb, int D, int fmt, const float *xg, const int *xoff, const int *nr,
@@ -998,6 +1043,7 @@ int mvllm_hip_init(int device) {
     for (auto &e : C.grp_done)
         HIP_TRY(hipEventCreateWithFlags(&e, kEvFlags));
     HIP_TRY(hipEventCreateWithFlags(&C.prev_done, kEvFlags));
+    HIP_TRY(hipEventCreateWithFlags(&C.miss_done, hipEventDisableTiming));
     C.device = device;
     C.ready = true;
     return 1;
@@ -1022,9 +1068,6 @@ void mvllm_hip_shutdown(void) {
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
-    C.sync.release();
-    C.sync_cap = 0;
-    C.cum.clear();
     C.hx.release();
     C.ho.release();
     for (auto &s : C.slots) {
@@ -1044,6 +1087,11 @@ void mvllm_hip_shutdown(void) {
     C.timed.clear();
     (void)hipEventDestroy(C.prev_done);
     C.prev_done = nullptr;
+    (void)hipEventDestroy(C.miss_done);
+    C.miss_done = nullptr;
+    for (void *p : g_retired)
+        (void)hipFree(p);
+    g_retired.clear();
     (void)hipStreamDestroy(C.own);
     (void)hipStreamDestroy(C.copy);
     C.have_last = false;
@@ -1073,13 +1121,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return 0;
         C.dec_ks = static_cast<int>(value);
-    } else if (k == "gemm_persist") {
-        gemm_set_persistent(value != 0);
-    } else if (k == "fuse") {
-        C.fuse = value ? 1 : 0;
     } else if (k == "dec_inline") {
         C.dec_inline = value ? 1 : 0;
-
     } else if (k == "combine_ordered") {
         C.combine_ordered = value ? 1 : 0;
     } else if (k == "fp4act") {
@@ -1116,26 +1159,8 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
         set_err("the device entry needs S > 0 (row count of out)");
         return 0;
     }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    Plan P;
-    build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
-    C.stats[0] += 1;
-    if (P.ew.empty())
-        return 1;
-    if (!order_after_previous(C, st))
-        return 0;
-    const size_t R = P.xrow.size();
-    HIP_TRY(C.H.ensure(std::max<size_t>(R * Iinter * 4, 256)));
-    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
-    CallCfg cc;
-    plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg);
-    DevPlan dp{};
-    if (!upload_plan(C, P, cc, st, dp, false))
-        return 0;
-    if (!run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
-                    P.ew.size(), nullptr))
-        return 0;
-    return finish_call(C, st, dp.slot);
+    return dev_call(C, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
+                    act, act_a, act_b, static_cast<hipStream_t>(stream));
 }
 
 int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,
@@ -1153,6 +1178,7 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     }
     if (!args_ok(nb, D, fmt, xg, xoff, nr, out))
         return 0;
+    HostClock hc(&C.stats[15]);
     Plan P;
     build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
     C.stats[0] += 1;
@@ -1264,7 +1290,8 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
                 }
             }
         }
-        HIP_TRY(hipEventCreateWithFlags(&miss_ev, hipEventDisableTiming));
+        // one event for every call: a wait takes the record current when it is enqueued
+        miss_ev = C.miss_done;
         HIP_TRY(hipEventRecord(miss_ev, C.copy));
     }
     // resident experts first, so their gate/up overlaps the miss copies
@@ -1292,14 +1319,14 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     std::vector<int> dest_rows = P.out_row;
     for (size_t t = 0; t < T; ++t)
         P.out_row[t] = static_cast<int>(t);
-    HIP_TRY(C.H.ensure(std::max<size_t>(R * Iinter * 4, 256)));
-    HIP_TRY(C.Y.ensure(std::max<size_t>(R * D * 4, 256)));
     CallCfg cc;
-    plan_call(C, cc, P, fmt, D, Iinter, hit.size(), C.Xc.p);
+    plan_call(C, cc, P, fmt, D, Iinter, hit.size(), C.Xc.p, true);
+    Bufs B;
+    HIP_TRY(get_bufs(C, cc, R, D, Iinter, B));
     DevPlan dp{};
     if (!upload_plan(C, P, cc, st, dp, true))
         return 0;
-    const int ok = run_phases(C, P, cc, dp, fmt, D, Iinter, act, act_a, act_b,
+    const int ok = run_phases(C, P, cc, dp, B, fmt, D, Iinter, act, act_a, act_b,
                               static_cast<const float *>(C.Xc.p), nullptr,
                               static_cast<float *>(C.Oc.p), st, hit.size(), miss_ev);
     if (!ok)
@@ -1313,8 +1340,6 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     if (!finish_call(C, st, dp.slot))
         return 0;
     HIP_TRY(hipStreamSynchronize(st));
-    if (miss_ev)
-        (void)hipEventDestroy(miss_ev);
     for (size_t t = 0; t < T; ++t)
         std::memcpy(out + (size_t)dest_rows[t] * D, static_cast<float *>(C.ho.p) + t * D,
                     (size_t)D * 4);
@@ -1435,22 +1460,18 @@ int mvllm_hip_stats(double *vals, int n) {
     Ctx &C = ctx();
     std::lock_guard<std::mutex> lk(C.mu);
     for (auto &t : C.timed) {
-        float ms[3] = {0, 0, 0};
-        (void)hipEventSynchronize(t.ev[3]);
-        for (int i = 0; i < 3; ++i)
+        float ms[5] = {0, 0, 0, 0, 0};
+        (void)hipEventSynchronize(t.ev[5]);
+        for (int i = 0; i < 5; ++i)
             (void)hipEventElapsedTime(&ms[i], t.ev[i], t.ev[i + 1]);
-        C.stats[9] += ms[0];
-        C.stats[10] += ms[1];
-        C.stats[11] += ms[2];
+        C.stats[12] += ms[0] + ms[2];
+        C.stats[9] += ms[1];
+        C.stats[10] += ms[3];
+        C.stats[11] += ms[4];
         for (auto &e : t.ev)
             (void)hipEventDestroy(e);
     }
     C.timed.clear();
-    if (C.sync.p) {  // waits of the fused launch that gave up (0 in a correct run)
-        int err = 0;
-        if (hipMemcpy(&err, C.sync.p, sizeof(int), hipMemcpyDeviceToHost) == hipSuccess)
-            C.stats[16] = err;
-    }
     const int m = std::min(n, 17);
     for (int i = 0; i < m; ++i)
         vals[i] = C.stats[i];
@@ -1461,7 +1482,7 @@ void mvllm_hip_stats_reset(void) {
     Ctx &C = ctx();
     std::lock_guard<std::mutex> lk(C.mu);
     for (auto &t : C.timed) {
-        (void)hipEventSynchronize(t.ev[3]);
+        (void)hipEventSynchronize(t.ev[5]);
         for (auto &e : t.ev)
             (void)hipEventDestroy(e);
     }

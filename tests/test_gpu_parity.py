@@ -284,6 +284,39 @@ def test_nonfinite_propagation(hip, orc, D, I):
         assert npref.rel_err(got[fin], exp[fin]) < TOL_F32
 
 
+@pytest.mark.parametrize("fmt", [4, 7])
+@pytest.mark.parametrize("path,D,I,gemm", [("elementwise", 256, 128, 0), ("decode", 512, 512, 2),
+                                           ("gemm", 512, 256, 1)])
+def test_clamp_swiglu_nonfinite_up(hip, orc, fmt, path, D, I, gemm):
+    """ClampSwiGLU with a non-finite up projection: the reference clamps `up` with
+    comparisons (src/quant/quant.hpp:37-50), so a NaN up stays NaN and reaches the row's
+    down outputs; an infinite one is clamped to +-limit.  The up scales alone carry the
+    non-finite values (MXFP4 byte 255 on a zero nibble gives 0 * inf = NaN; an int4 scale
+    of inf or NaN), on the element-wise, decode and grouped-GEMM paths."""
+    say("clamp nonfinite up", fmt, path)
+    rng = np.random.default_rng(19 + fmt + D)
+    c = random_case(rng, fmt, D, I, [2, 1, 3], 6, 1, 7.0, 0.0)
+    c.rows[:] = np.arange(6, dtype=np.int32)
+    if fmt == 7:
+        c.us[0][3, 1] = 255            # +inf block scale: NaN where the nibble is +-0
+        c.us[2][5, 0] = 255
+    else:
+        c.us[0][3, 1] = np.nan
+        c.us[2][5, 0] = np.inf
+    assert hip.set_option("gemm", gemm)
+    try:
+        got = run_dev(hip, c, 1, 7.0, 0.0)
+    finally:
+        hip.set_option("gemm", 0)
+    exp = oracle_out(orc, c, 1, 7.0, 0.0)
+    assert np.isnan(exp).any()  # the case reaches the clamp with a NaN up
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    fin = np.isfinite(exp)
+    tol = TOL_F32 if gemm != 1 else 1e-2
+    assert npref.rel_err(got[fin], exp[fin]) < tol
+
+
 # ------------------------------------------------------------- benchmark configs
 
 @pytest.mark.parametrize("name,T", [("c0", 1), ("c1", 1), ("c1", 4), ("c1", 16), ("c2", 1)])
@@ -444,23 +477,6 @@ def test_gemm_parity(hip, case, mode, tol):
             assert np.array_equal(got[t], c.out[t])
 
 
-@pytest.mark.parametrize("case", [GEMM_CASES[0], GEMM_CASES[3], GEMM_CASES[4]])
-def test_gemm_persistent_option(hip, case):
-    """Option gemm_persist=1 (persistent workgroups prefetching across tasks) gives the
-    same sums as the default one-workgroup-per-task launch: same tiles, same order."""
-    fmt, D, I, nr, S, act, a, b, nulls, bad = case
-    say("gemm persist", case)
-    rng = np.random.default_rng(D * 17 + I + sum(nr))
-    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
-    base = _gemm_run(hip, c, 0)
-    assert hip.set_option("gemm_persist", 1)
-    try:
-        got = _gemm_run(hip, c, 0)
-    finally:
-        hip.set_option("gemm_persist", 0)
-    assert np.array_equal(got, base)
-
-
 @pytest.mark.parametrize("fmt,D,I,nr,act,a,b", [
     (4, 6144, 2048, [40, 21, 1], 1, 7.0, 0.0),          # c3 shapes
     (7, 7168, 2048, [130, 3, 17], 2, 4.0, 25.0),         # c4 shapes, a full 128-row block
@@ -607,60 +623,10 @@ def test_combine_ordered_vs_atomic(hip, orc, case):
     for t in range(c.out.shape[0]):
         if t not in touched:
             assert np.array_equal(got_a[t], c.out[t])
-
-
-# ------------------------------------------------------------- fused decode launch
-
-@pytest.mark.parametrize("case", [DEV_CASES[0], DEV_CASES[1], DEV_CASES[2], DEV_CASES[7],
-                                  DEV_CASES[8]])
-def test_fused_vs_two_launches(hip, orc, case):
-    """Option fuse=1: decode calls with every expert resident run both projections in one
-    cooperative launch; the down tasks wait on per-expert counters that the gate/up tasks
-    advance once their H is stored.  Same arithmetic as the two launches (the default);
-    both meet the decode bar and no wait gives up."""
-    fmt, D, I, nr, S, act, a, b, nulls, bad = case
-    say("fused", case)
-    rng = np.random.default_rng(D * 7 + I + len(nr))
-    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
-    exp = oracle_out(orc, c, act, a, b)
-    hip.stats_reset()
-    assert hip.set_option("fuse", 1)
-    try:
-        got_f = run_dev(hip, c, act, a, b)
-    finally:
-        hip.set_option("fuse", 0)
-    st = hip.stats()
-    say("  fused launches", st["launches_fused"])
-    assert st["launches_fused"] == 1  # every case here has a fused-eligible shape
-    got_u = run_dev(hip, c, act, a, b)
-    for got in (got_f, got_u):
-        assert npref.rel_err(got, exp) < TOL_F32
-    assert npref.rel_err(got_f, got_u) < TOL_F32
-    assert hip.stats()["sync_timeouts"] == 0
-
-
-def test_fused_call_sequence(hip, orc):
-    """Calls in a row with changing expert counts -- including more experts than the
-    counters first held (they are reallocated and restart) -- keep every down task
-    waiting for exactly its own call's gate/up tasks."""
-    say("fused sequence")
-    rng = np.random.default_rng(1234)
-    for i, (fmt, nb, S) in enumerate([(4, 3, 2), (7, 9, 4), (4, 300, 64), (4, 5, 3),
-                                      (7, 290, 40), (4, 2, 1)]):
-        nr = list(rng.integers(1, 3, size=nb))
-        c = random_case(rng, fmt, 512, 512, nr, S, 1 if fmt == 4 else 2,
-                        7.0 if fmt == 4 else 4.0, 0.0 if fmt == 4 else 25.0)
-        act, a, b = (1, 7.0, 0.0) if fmt == 4 else (2, 4.0, 25.0)
-        hip.stats_reset()
-        assert hip.set_option("fuse", 1)
-        try:
-            got = run_dev(hip, c, act, a, b)
-        finally:
-            hip.set_option("fuse", 0)
-        st = hip.stats()
-        exp = oracle_out(orc, c, act, a, b)
-        err = npref.rel_err(got, exp)
-        say("  call", i, "nb", nb, "fused", st["launches_fused"], "rel_err", err)
-        assert st["launches_fused"] == 1
-        assert err < TOL_F32
-    assert hip.stats()["sync_timeouts"] == 0
+    # the host-pointer drop-in always combines in the reference's order: two calls give
+    # bit-identical results, equal to the ordered device call's
+    h1, h2 = c.out.copy(), c.out.copy()
+    hip.moe_block(*c.args(h1), act, a, b)
+    hip.moe_block(*c.args(h2), act, a, b)
+    assert np.array_equal(h1.view(np.uint32), h2.view(np.uint32))
+    assert np.array_equal(h1.view(np.uint32), got_o.view(np.uint32))
