@@ -84,6 +84,29 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
                             const int *nr, const int *rows, const float *rw, float *out, int S,
                             int act, float act_a, float act_b, void *stream);
 
+/* No counterpart in the reference.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * mvllm_hip_moe_block_dev with the same arguments, results and ordering rules, except
+ * that it allocates no device or pinned memory (hipMalloc, hipHostMalloc, hipFree or
+ * the like; host-side planning still uses the C++ heap).  Its device scratch is one
+ * 48 MiB array per device, held from mvllm_hip_init until the process ends: the plan's
+ * device copy (at most 256 KiB, about 450 decode items) and the call's buffers (at most
+ * 47.75 MiB; decode calls need about R * Iinter * 4.1 bytes with the default
+ * arithmetic, or R * (Iinter * 4.1 + D * 4) with combine_ordered, grouped-GEMM calls
+ * R * (2 * D + 2 * Iinter + 4 * D), for R routed rows).  A call beyond either limit
+ * returns 0 with a message in mvllm_hip_last_error and enqueues nothing.  Every call on
+ * a device shares that device's array and the array keeps the last call's contents:
+ * calls ordered by this library (one stream, or the library's own ordering across
+ * streams) are safe; calls that overlap on one device from outside that ordering race.
+ * Option "timing" is ignored by this entry. */
+int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
+                                    const void *const *g, const void *const *u,
+                                    const void *const *d, const float *const *gs,
+                                    const float *const *us, const float *const *ds,
+                                    const float *xg, const int *xoff, const int *nr,
+                                    const int *rows, const float *rw, float *out, int S, int act,
+                                    float act_a, float act_b, void *stream);
+
 /* Options (key, value), process-wide; returns 1 if the key and value are accepted.
  *   "mode"   how activations enter the bf16 matrix cores (weights are always decoded
  *            exactly; products and sums are f32):

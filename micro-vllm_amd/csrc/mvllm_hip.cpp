@@ -156,6 +156,7 @@ struct Ctx {
     // recorded is a queue packet that idles the GPU between two calls' kernels (~4.6 us).
     hipEvent_t prev_done = nullptr;
     hipEvent_t miss_done = nullptr;  // the staged path's miss copies (copy stream)
+    void *scratch_ptr = nullptr;     // device address of `scratch` on `device`
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     HostBuf hx, ho;
@@ -193,6 +194,15 @@ Ctx &ctx() {
     static Ctx c;
     return c;
 }
+
+// ---- device memory of the no-allocation entry (mvllm_hip_moe_block_dev_noalloc) -----
+// One array per device, held until the process ends: the plan's device copy in the first
+// kScratchPlan bytes, then the call's buffers.  Host code must not pass `scratch` itself
+// to a kernel or a copy (in host code it names a host-side stand-in): mvllm_hip_init
+// looks up its device address with hipGetSymbolAddress and keeps it in Ctx::scratch_ptr.
+constexpr size_t kScratchBytes = size_t(48) << 20;
+constexpr size_t kScratchPlan = size_t(256) << 10;
+static __device__ __attribute__((aligned(256))) char scratch[kScratchBytes];
 
 // Host time spent inside an entry point, added to stats[15] (ms) when the scope ends.
 struct HostClock {
@@ -543,7 +553,9 @@ hipError_t get_bufs(Ctx &C, const CallCfg &cc, size_t R, int D, int I, Bufs &B) 
 }
 
 // Upload the plan (experts, xrow, combine CSR, items) through a pinned slot; returns
-// device pointers into the slot's device buffer.
+// device pointers into the slot's device buffer, or into dev_dst (dev_cap bytes) when
+// given, in which case nothing is allocated: the slot's pinned buffer must already hold
+// the plan.
 struct DevPlan {
     ExpertWork *ew;
     int *xrow, *tok_ptr, *ent_row, *out_row, *items, *rdest;
@@ -614,7 +626,7 @@ bool compact_desc(const DecDesc *d, int n, DecDescK *k) {
 }
 
 int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPlan &dp,
-                bool rows_identity) {
+                bool rows_identity, void *dev_dst = nullptr, size_t dev_cap = 0) {
     if (C.open_last >= 0) {  // a group's last call stopped early: its event is stale
         HIP_TRY(hipDeviceSynchronize());
         C.grp_used[C.open_last / Ctx::kGroup] = false;
@@ -639,9 +651,20 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t n_dn = cc.mfma ? cc.dn.it1 - cc.dn.it0 : 0;
     const size_t b_dg = n_gu * sizeof(DecDesc), b_dd = n_dn * sizeof(DecDesc);
     const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw + b_dg + b_dd;
-    HIP_TRY(s.host.ensure(total));
-    HIP_TRY(s.dev.ensure(total));
-    char *dbase = static_cast<char *>(s.dev.p);
+    if (dev_dst) {
+        if (total > s.host.cap || total > dev_cap) {
+            set_err("plan of " + std::to_string(total) + " bytes exceeds the preallocated " +
+                    std::to_string(std::min(s.host.cap, dev_cap)) + "-byte plan buffers");
+            if (si % Ctx::kGroup == Ctx::kGroup - 1)
+                C.open_last = -1;  // nothing of this call was enqueued
+            C.slot_next = si;
+            return 0;
+        }
+    } else {
+        HIP_TRY(s.host.ensure(total));
+        HIP_TRY(s.dev.ensure(total));
+    }
+    char *dbase = dev_dst ? static_cast<char *>(dev_dst) : static_cast<char *>(s.dev.p);
     char *h = static_cast<char *>(s.host.p);
     size_t o = 0;
     auto put = [&](const void *src, size_t n, size_t b) {
@@ -756,8 +779,8 @@ GemvArgs generic_args(const DevPlan &dp, size_t first, size_t count, const int *
 int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, const Bufs &B,
                int fmt, int D, int I, int act, float a, float b, const float *in,
                const int *in_rows, float *out, hipStream_t st, size_t split,
-               hipEvent_t gate_event) {
-    const bool timing = C.timing != 0;  // per-phase events (created per call)
+               hipEvent_t gate_event, bool timed = true) {
+    const bool timing = C.timing && timed;  // per-phase events (created per call)
     const size_t n = P.ew.size(), R = P.xrow.size();
     const int rcap = static_cast<int>(R);
     TimedCall tc{};
@@ -927,12 +950,14 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
     return 1;
 }
 
-// One mvllm_hip_moe_block_dev call (arguments validated).
+// One mvllm_hip_moe_block_dev call (arguments validated).  noalloc: every device buffer
+// comes from the scratch array (the plan's copy first, then the call's Bufs), nothing is
+// allocated, calls that do not fit are refused, and option "timing" is ignored.
 int dev_call(Ctx &C, int nb, int D, int Iinter, int fmt, const void *const *g,
              const void *const *u, const void *const *d, const float *const *gs,
              const float *const *us, const float *const *ds, const float *xg, const int *xoff,
              const int *nr, const int *rows, const float *rw, float *out, int S, int act,
-             float act_a, float act_b, hipStream_t st) {
+             float act_a, float act_b, hipStream_t st, bool noalloc) {
     HostClock hc(&C.stats[15]);
     Plan P;
     build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
@@ -943,14 +968,33 @@ int dev_call(Ctx &C, int nb, int D, int Iinter, int fmt, const void *const *g,
     CallCfg cc;
     plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg, C.combine_ordered != 0);
     Bufs B;
+    if (noalloc) {  // carve the buffers out of the scratch array, after the plan region
+        size_t sz[5], off = kScratchPlan;
+        buf_sizes(cc, R, D, Iinter, sz);
+        void **dst[5] = {&B.H, &B.Y, &B.Ph, &B.HP, &B.Xp};
+        for (int i = 0; i < 5; ++i) {
+            if (!sz[i])
+                continue;
+            *dst[i] = static_cast<char *>(C.scratch_ptr) + off;
+            off += (sz[i] + 255) & ~size_t(255);
+        }
+        if (off > kScratchBytes) {
+            set_err("call needs " + std::to_string(off - kScratchPlan) +
+                    " bytes of scratch; the no-allocation entry holds " +
+                    std::to_string(kScratchBytes - kScratchPlan));
+            return 0;
+        }
+    }
     if (!order_after_previous(C, st))
         return 0;
-    HIP_TRY(get_bufs(C, cc, R, D, Iinter, B));
+    if (!noalloc)
+        HIP_TRY(get_bufs(C, cc, R, D, Iinter, B));
     DevPlan dp{};
-    if (!upload_plan(C, P, cc, st, dp, false))
+    if (!upload_plan(C, P, cc, st, dp, false, noalloc ? C.scratch_ptr : nullptr,
+                     noalloc ? kScratchPlan : 0))
         return 0;
     if (!run_phases(C, P, cc, dp, B, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
-                    P.ew.size(), nullptr))
+                    P.ew.size(), nullptr, !noalloc))
         return 0;
     return finish_call(C, st, dp.slot);
 }
@@ -1034,6 +1078,10 @@ int mvllm_hip_init(int device) {
         return 0;
     }
     HIP_TRY(hipSetDevice(device));
+    // the no-allocation entry's device array, and its pinned plan slots, sized up front
+    HIP_TRY(hipGetSymbolAddress(&C.scratch_ptr, HIP_SYMBOL(scratch)));
+    for (auto &s : C.slots)
+        HIP_TRY(s.host.ensure(kScratchPlan));
     HIP_TRY(hipStreamCreateWithFlags(&C.own, hipStreamNonBlocking));
     HIP_TRY(hipStreamCreateWithFlags(&C.copy, hipStreamNonBlocking));
     // The plan-slot and ordering events order the host's reuse of a slot and other streams
@@ -1092,6 +1140,7 @@ void mvllm_hip_shutdown(void) {
     for (void *p : g_retired)
         (void)hipFree(p);
     g_retired.clear();
+    C.scratch_ptr = nullptr;
     (void)hipStreamDestroy(C.own);
     (void)hipStreamDestroy(C.copy);
     C.have_last = false;
@@ -1160,7 +1209,32 @@ int mvllm_hip_moe_block_dev(int nb, int D, int Iinter, int fmt, int qgs, const v
         return 0;
     }
     return dev_call(C, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
-                    act, act_a, act_b, static_cast<hipStream_t>(stream));
+                    act, act_a, act_b, static_cast<hipStream_t>(stream), false);
+}
+
+int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
+                                    const void *const *g, const void *const *u,
+                                    const void *const *d, const float *const *gs,
+                                    const float *const *us, const float *const *ds,
+                                    const float *xg, const int *xoff, const int *nr,
+                                    const int *rows, const float *rw, float *out, int S, int act,
+                                    float act_a, float act_b, void *stream) {
+    (void)qgs;
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !C.scratch_ptr) {
+        set_err("mvllm_hip_init not called");
+        return 0;
+    }
+    if (!args_ok(nb, D, fmt, xg, xoff, nr, out))
+        return 0;
+    if (S <= 0) {
+        set_err("the device entry needs S > 0 (row count of out)");
+        return 0;
+    }
+    return dev_call(C, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out, S,
+                    act, act_a, act_b, static_cast<hipStream_t>(stream), true);
 }
 
 int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void *const *g,

@@ -42,6 +42,8 @@ _SIGS = {
                                  _p, _p, _i, _i, _f, _f]),
     "mvllm_hip_moe_block_dev": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p, _p,
                                      _p, _p, _p, _p, _i, _i, _f, _f, _p]),
+    "mvllm_hip_moe_block_dev_noalloc": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp,
+                                             _p, _p, _p, _p, _p, _p, _i, _i, _f, _f, _p]),
     "mvllm_hip_set_option": (_i, [C.c_char_p, _ll]),
     "mvllm_moe_union_ids": (_i, [_p, _i, _i, _p, _i]),
     "mvllm_moe_segments": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
@@ -154,6 +156,21 @@ def moe_block_dev(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, r
                                        act_b, st)
     if check:
         _check(rc, "mvllm_hip_moe_block_dev")
+    return rc
+
+
+def moe_block_dev_noalloc(nb, D, Iinter, fmt, g, u, d, gs, us, ds, xg, xoff, nr, rows, rw, out,
+                          S, act=ACT_SILU, act_a=0.0, act_b=0.0, stream=None, check=True,
+                          prepared=None):
+    """mvllm_hip_moe_block_dev_noalloc: moe_block_dev's arguments, no device allocation."""
+    pa = prepared if prepared is not None else \
+        [None if L is None else _ptr_array(L) for L in (g, u, d, gs, us, ds)]
+    st = None if stream is None else (stream if isinstance(stream, int) else stream.cuda_stream)
+    rc = lib().mvllm_hip_moe_block_dev_noalloc(nb, D, Iinter, fmt, 0, *pa, _ptr(xg), _ptr(xoff),
+                                               _ptr(nr), _ptr(rows), _ptr(rw), _ptr(out), S, act,
+                                               act_a, act_b, st)
+    if check:
+        _check(rc, "mvllm_hip_moe_block_dev_noalloc")
     return rc
 
 
