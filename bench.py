@@ -1,13 +1,19 @@
 """moe_block benchmark on one MI355X.
 
-Default workload: config c1 (OLMoE shape, int4-g64, D=2048, I=1024, 64 experts,
-top-8, SwiGLU) at T=16 decode tokens.  One step = one mvllm_hip_moe_block_dev call
-(gate/up/act GEMV, down GEMV, top-k combine) with weights, activations and output
-already resident in HBM.  Every step reads its experts from a different layer of a
->= 4 GiB weight pool, so the 256 MB Infinity Cache cannot serve repeated weights.
+Headline workload: config c4, the largest single-GPU configuration (K3-style MXFP4
+prefill, D=7168, I=2048, 384 experts, top-8, T=2048 tokens, Zipf(1.1) routing, SiTU)
+through mvllm_hip_moe_block_dev with weights, activations and output resident in HBM.
+One step = one call: the bf16 grouped GEMM over the token-sorted expert segments (gate/up
++ activation, down) and the top-k combine in the reference's order.  The same run also
+reports, under "extra": c4 on native MXFP4 activations (scaled FP4 matrix cores), c0,
+c1 at T=1/4/16, c2 (resident, and through the drop-in host entry with 25% of its experts
+staged from pinned host memory) and c3.  Every timed call reads its experts from a weight
+pool of >= 4 GiB (a whole c3/c4 call reads >= 5.4 GB), so the 256 MB Infinity Cache
+cannot serve repeated weights.
 
 Prints ONE JSON line on stdout; details go to stderr.
-  python bench.py [--steps K] [--warmup W] [--config c1] [--tokens T] [--mode M]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c4] [--tokens T]
+                  [--fp4act] [--no-extra] [--no-cpu]
 """
 import argparse
 import json
@@ -19,77 +25,208 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "micro-vllm_amd"))
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
-HBM_PEAK_GBS = 8000.0
-FP4_PEAK_TFS = 10100.0
-BF16_PEAK_TFS = 2500.0
-
-
-def traffic_bytes(workload, phase):
-    """HBM bytes per launch of the workload's gate/up kernel as measured with rocprofv3
-    FETCH_SIZE / WRITE_SIZE runs (profiles/traffic.json, calibrated against a copy of
-    known size), or None when that workload has not been measured."""
-    try:
-        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
-            d = json.load(f)
-    except (OSError, ValueError):
-        return None
-    for k, v in d.get(workload, {}).items():
-        if k.endswith(phase):
-            return v.get("bytes")
-    return None
+HBM_PEAK_GBS = 8000.0     # MI355X HBM3E
+FP4_PEAK_TFS = 10100.0    # dense MXFP4 matrix cores
+BF16_PEAK_TFS = 2500.0    # dense bf16 matrix cores
+METRIC = "moe_block tokens/s + effective weight GB/s (decode), MFMA util (prefill)"
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def traffic_bytes(workload, kernel):
+    """HBM bytes per call of `kernel` in `workload` from rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs (profiles/traffic.json, each counter calibrated by a copy of known size), or None
+    when that pair has not been measured."""
+    try:
+        with open(os.path.join(ROOT, "profiles", "traffic.json")) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    v = d.get(workload, {}).get(kernel)
+    return None if v is None else v.get("bytes")
+
+
+def expert_bytes(fmt, D, I):
+    """Algorithmic bytes of one expert in the reference layout: (gate + up, down)."""
+    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+    gu = 2 * (I * ((D + 1) // 2) + I * ((D + gq - 1) // gq) * sb)
+    dn = D * ((I + 1) // 2) + D * ((I + gq - 1) // gq) * sb
+    return gu, dn
+
+
+def binding_roof_us(nr, bytes_e, flops_per_row, peak_tfs):
+    """t_lb = sum over experts of max(bytes_e / HBM peak, flops_e / matrix-core peak), us."""
+    t = 0.0
+    for n in nr:
+        t += max(bytes_e / (HBM_PEAK_GBS * 1e9), flops_per_row * float(n) / (peak_tfs * 1e12))
+    return t * 1e6
+
+
 def build_pool(torch, mvllm_hip, fmt, D, I, n_blobs, seed):
     """n_blobs expert blobs in the reference layout, generated on the GPU."""
+    from mvllm_hip import synth
     nbytes, off = mvllm_hip.expert_geom(fmt, D, I)
-    stride = (nbytes + 255) // 256 * 256
-    g = torch.Generator(device="cuda").manual_seed(seed)
-    pool = torch.randint(0, 256, (n_blobs, stride), dtype=torch.uint8, device="cuda",
-                         generator=g)
-    gq = 64 if fmt == 4 else 32
-    pieces = [(1, I, D), (3, I, D), (5, D, I)]  # scale pieces: (offset index, rows O, K)
-    for oi, O, K in pieces:
-        ns = O * ((K + gq - 1) // gq)
-        o = int(off[oi])
-        if fmt == 4:
-            s = torch.empty((n_blobs, ns), dtype=torch.float32, device="cuda")
-            s.uniform_(0.005, 0.02, generator=g)
-            s = s.to(torch.bfloat16).to(torch.float32)  # bf16-valued scales stored as f32
-            pool[:, o:o + 4 * ns] = s.view(torch.uint8).view(n_blobs, 4 * ns)
-        else:
-            pool[:, o:o + ns] = torch.randint(118, 125, (n_blobs, ns), dtype=torch.uint8,
-                                              device="cuda", generator=g)
+    pool, stride = synth.device_pool(torch, fmt, D, I, n_blobs, seed, (nbytes, off))
     return pool, stride, off, nbytes
+
+
+class Pool:
+    """A weight pool for one configuration: `layers` layers of the workload's nb experts,
+    rotated per step, together at least pool_gb (or one layer when that is larger)."""
+
+    def __init__(self, np, torch, mvllm_hip, w, fmt, D, I, pool_gb, seed=1234):
+        nbytes, _ = mvllm_hip.expert_geom(fmt, D, I)
+        self.layers = max(1, int(np.ceil(pool_gb * 2**30 / (nbytes * w.nb))))
+        self.n_blobs = self.layers * w.nb
+        self.pool, self.stride, self.off, self.nbytes = build_pool(torch, mvllm_hip, fmt, D, I,
+                                                                   self.n_blobs, seed)
+        base = self.pool.data_ptr()
+        order = (0, 2, 4, 1, 3, 5)  # geometry offsets: gate_p gate_s up_p up_s down_p down_s
+        self.lists = []
+        for layer in range(self.layers):
+            ptrs = [[], [], [], [], [], []]
+            for i in range(w.nb):
+                b = base + (layer * w.nb + i) * self.stride
+                for slot, oi in enumerate(order):
+                    ptrs[slot].append(b + int(self.off[oi]))
+            self.lists.append(mvllm_hip.prepare_lists(*ptrs))
+        self.gib = self.n_blobs * self.nbytes / 2**30
+
+
+def measure(np, torch, mvllm_hip, synth, name, T, steps, warmup, pool_gb, fp4act=False,
+            pool=None, w=None, cpu_seconds=0.0):
+    """Times `steps` moe_block_dev calls of workload (name, T) after `warmup`, then a second
+    pass with the library's per-phase HIP events (recorded on the stream the kernels run
+    on).  Returns (record, pool, workload)."""
+    cfg = synth.CONFIGS[name]
+    D, I, fmt = cfg["D"], cfg["I"], cfg["fmt"]
+    if w is None:
+        w = synth.make_workload(name, T=T, with_experts=False)
+    if pool is None:
+        pool = Pool(np, torch, mvllm_hip, w, fmt, D, I, pool_gb)
+    mvllm_hip.set_option("fp4act", 1 if fp4act else 0)
+    xg = torch.from_numpy(w.xg).cuda()
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    addr = [xg.data_ptr()] + [a.ctypes.data for a in (w.xoff, w.nr, w.rows, w.rw)] + \
+        [out.data_ptr()]
+
+    def step(s):
+        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, *addr[:5],
+                                addr[5], T, w.act, w.a, w.b,
+                                prepared=pool.lists[s % pool.layers])
+
+    for s in range(warmup):
+        step(s)
+    torch.cuda.synchronize()
+    # timed region: `steps` calls bracketed by synchronize; torch's stream is the null
+    # stream, which the library's kernels run on
+    st0 = mvllm_hip.stats()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for s in range(steps):
+        step(s)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / steps
+    st1 = mvllm_hip.stats()
+    host_us = (st1["host_ms"] - st0["host_ms"]) / steps * 1e3
+    wait_us = (st1["host_wait_ms"] - st0["host_wait_ms"]) / steps * 1e3
+    # per-phase kernel durations: a second pass with HIP events around each phase
+    mvllm_hip.set_option("timing", 1)
+    mvllm_hip.stats_reset()
+    for s in range(steps):
+        step(s)
+    torch.cuda.synchronize()
+    st = mvllm_hip.stats()
+    mvllm_hip.set_option("timing", 0)
+    mvllm_hip.set_option("fp4act", 0)
+    ph = {k: st["ms_" + k] / steps * 1e3 for k in ("prep", "gate_up", "down", "combine")}
+
+    nr = [int(n) for n in w.nr]
+    rows = int(sum(nr))
+    gemm = max(nr) > 16 or fp4act
+    if fp4act and fmt == 7:
+        dtype, peak = "mxfp4", FP4_PEAK_TFS
+    else:
+        dtype, peak = ("bf16" if gemm else "bf16x2"), BF16_PEAK_TFS
+    b_gu, b_dn = expert_bytes(fmt, D, I)
+    wbytes = w.nb * (b_gu + b_dn)
+    flops = 6.0 * D * I * rows
+    t_gu = ph["gate_up"]
+    gu_gbs = w.nb * b_gu / (t_gu * 1e-6) / 1e9
+    lb_gu = binding_roof_us(nr, b_gu, 4.0 * D * I, peak)
+    lb_call = binding_roof_us(nr, b_gu + b_dn, 6.0 * D * I, peak)
+    wl = f"{name} T={T}" + (" fp4act" if fp4act else "")
+    kern = ("k_gemm_fp4 gate/up" if fp4act else "k_gemm gate/up") if gemm else \
+        "k_mfma_dec gate/up"
+    rec = {
+        "workload": f"{name} {cfg['desc']}, T={T}" + (", native MXFP4 activations" if fp4act else ""),
+        "value": round(T / (ms_step * 1e-3), 2), "unit": "tokens/s",
+        "ms_per_step": round(ms_step, 6), "wall_ms_per_step": round(wall / steps * 1e3, 6),
+        "host_us_per_call": round(host_us - wait_us, 1),
+        "host_wait_us_per_call": round(wait_us, 1), "dtype": dtype,
+        "experts": int(w.nb), "rows": rows, "max_rows_per_expert": int(max(nr)),
+        "weight_gbps": round(wbytes / (ms_step * 1e-3) / 1e9, 1),
+        "weight_bytes": int(wbytes), "flops": flops,
+        "mfma_util": {"bf16": round(flops / (ms_step * 1e-3) / (BF16_PEAK_TFS * 1e12), 5),
+                      "fp4": round(flops / (ms_step * 1e-3) / (FP4_PEAK_TFS * 1e12), 5)},
+        "phases_us": {k: round(v, 3) for k, v in ph.items()},
+        "kernel_sum_us": round(sum(ph.values()), 3),
+        "roofline": {
+            "bound": "hbm", "kernel": kern + (" (all row classes of one call)" if gemm else ""),
+            "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_bytes(wl, "gate_up"),
+            "bytes_per_launch": int(w.nb * b_gu), "avg_launch_us": round(t_gu, 3),
+            "binding": {"t_lb_us": round(lb_gu, 2), "frac": round(lb_gu / t_gu, 4),
+                        "peak_tflops": peak,
+                        "rule": "sum over experts of max(gate/up bytes / 8 TB/s, "
+                                "4 D I rows / matrix-core peak)"},
+        },
+        "call_binding": {"t_lb_us": round(lb_call, 2), "t_us": round(ms_step * 1e3, 2),
+                         "frac": round(lb_call / (ms_step * 1e3), 4)},
+        "pool_gib": round(pool.gib, 2),
+    }
+    log(f"[{wl}] step {ms_step*1e3:.1f} us (wall {wall/steps*1e6:.1f} us, host "
+        f"{host_us - wait_us:.1f} us/call + {wait_us:.1f} us blocked on the device): prep {ph['prep']:.1f}, gate/up {t_gu:.1f}, down "
+        f"{ph['down']:.1f}, combine {ph['combine']:.1f} us; gate/up {gu_gbs:.0f} GB/s "
+        f"(binding roof {lb_gu:.1f} us, {lb_gu/t_gu:.3f}); call {lb_call/(ms_step*1e3):.3f} "
+        f"of its binding roof; MFMA util bf16 {rec['mfma_util']['bf16']:.3f} fp4 "
+        f"{rec['mfma_util']['fp4']:.4f}")
+    if cpu_seconds > 0:
+        rec["cpu_baseline"] = cpu_baseline(np, torch, w, pool.pool, pool.stride, pool.off, fmt,
+                                           D, I, T, cpu_seconds)
+    del xg, out
+    return rec, pool, w
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="c1")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c4")
     ap.add_argument("--tokens", type=int, default=None)
     ap.add_argument("--mode", type=int, default=0)
     ap.add_argument("--opt", action="append", default=[], metavar="KEY=VALUE",
                     help="extra mvllm_hip_set_option settings (e.g. dec_ks=2)")
     ap.add_argument("--fp4act", action="store_true",
-                    help="MXFP4 experts: quantize activations, native scaled-FP4 matrix cores")
+                    help="headline on native MXFP4 activations (scaled-FP4 matrix cores)")
     ap.add_argument("--pool-gb", type=float, default=4.5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="only the headline workload (profiling runs)")
     ap.add_argument("--probe-sizes", action="store_true",
                     help="also time the stream-read probe at launch-sized reads (8 MiB .. "
-                         "1 GiB, each repetition at a new offset of the pool, so no read is "
-                         "served by the Infinity Cache): the floor one launch of that many "
-                         "bytes can reach")
+                         "1 GiB, each repetition at a new offset of the pool)")
     ap.add_argument("--staged", type=float, default=None, metavar="MISS_RATE",
-                    help="drop-in host entry with the HBM expert tier: this fraction of each "
-                         "step's experts is not resident and is copied from pinned host "
-                         "memory by the call (config c2 uses 0.25)")
+                    help="only the drop-in host entry with the HBM expert tier: this fraction "
+                         "of each step's experts is copied from pinned host memory by the call")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -105,179 +242,108 @@ def main():
 
     cfg = dict(synth.CONFIGS[args.config])
     T = args.tokens or cfg["T"]
-    D, I, E, k, fmt = cfg["D"], cfg["I"], cfg["E"], cfg["k"], cfg["fmt"]
     mvllm_hip.init(0)
     mvllm_hip.set_option("mode", args.mode)
-    mvllm_hip.set_option("fp4act", 1 if args.fp4act else 0)
     for kv in args.opt:
         k, v = kv.split("=", 1)
         if not mvllm_hip.set_option(k, int(v)):
             raise SystemExit(f"option {kv} refused")
-
     if args.staged is not None:
-        return staged(args, np, torch, mvllm_hip, synth, cfg, T)
+        print(json.dumps(staged(args, np, torch, mvllm_hip, synth, cfg, T, args.steps,
+                                args.warmup, args.staged,
+                                0.0 if args.no_cpu else args.cpu_seconds)), flush=True)
+        return
 
-    w = synth.make_workload(args.config, T=T, with_experts=False)
-    nbytes, _ = mvllm_hip.expert_geom(fmt, D, I)
-    layers = max(1, int(np.ceil(args.pool_gb * 2**30 / (nbytes * w.nb))))
-    n_blobs = layers * w.nb
-    log(f"workload {args.config} T={T}: {w.nb} experts, {int(w.nr.sum())} rows, "
-        f"{layers} pool layers x {w.nb} blobs of {nbytes/2**20:.2f} MiB "
-        f"({n_blobs * nbytes / 2**30:.2f} GiB)")
-    pool, stride, off, _ = build_pool(torch, mvllm_hip, fmt, D, I, n_blobs, 1234)
-    base = pool.data_ptr()
-
-    def lists(layer):
-        ptrs = [[], [], [], [], [], []]  # g, u, d, gs, us, ds
-        order = (0, 2, 4, 1, 3, 5)       # geometry offsets: gate_p gate_s up_p up_s down_p down_s
-        for i in range(w.nb):
-            b = base + (layer * w.nb + i) * stride
-            for slot, oi in enumerate(order):
-                ptrs[slot].append(b + int(off[oi]))
-        return ptrs
-
-    layer_lists = [mvllm_hip.prepare_lists(*lists(l)) for l in range(layers)]
-    xg = torch.from_numpy(w.xg).cuda()
-    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
-    xoff, nr, rows, rw = w.xoff, w.nr, w.rows, w.rw
-    # the same arrays every step: their addresses are looked up once (w keeps them alive)
-    addr = [xg.data_ptr()] + [a.ctypes.data for a in (xoff, nr, rows, rw)] + [out.data_ptr()]
-
-    def step(s):
-        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, *addr[:5],
-                                addr[5], T, w.act, w.a, w.b, prepared=layer_lists[s % layers])
-
-    for s in range(args.warmup):
-        step(s)
-    torch.cuda.synchronize()
-
-    # timed region: K steps bracketed by synchronize (torch's stream = the null stream,
-    # which the library's kernels run on)
-    t0 = time.perf_counter()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for s in range(args.steps):
-        step(s)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = ev0.elapsed_time(ev1) / args.steps
-
-    # per-kernel durations: a second pass with the library's HIP events around each
-    # phase, recorded on the stream the kernels are launched on
-    mvllm_hip.set_option("timing", 1)
-    mvllm_hip.stats_reset()
-    for s in range(args.steps):
-        step(s)
-    torch.cuda.synchronize()
-    st = mvllm_hip.stats()
-    mvllm_hip.set_option("timing", 0)
-    ms_gu = st["ms_gate_up"] / args.steps
-    ms_dn = st["ms_down"] / args.steps
-    ms_cb = st["ms_combine"] / args.steps
-
-    # arithmetic of the path the library picks (mvllm_hip.cpp plan_call): native FP4 when
-    # asked for; bf16 activations in the grouped GEMM (some expert > 16 rows); otherwise
-    # the decode kernels' f32 split into two bf16 terms
-    if args.fp4act and fmt == 7:
-        dtype = "mxfp4"
-    elif int(w.nr.max()) > 16:
-        dtype = "bf16" if args.mode != 1 else "bf16x2"
-    else:
-        dtype = {0: "bf16x2", 1: "bf16x3", 2: "bf16"}[args.mode]
-    gq, sb = (64, 4) if fmt == 4 else (32, 1)
-    b_gu = 2 * (I * (D // 2) + I * ((D + gq - 1) // gq) * sb)   # gate + up, one expert
-    b_dn = D * (I // 2) + D * ((I + gq - 1) // gq) * sb          # down, one expert
-    wbytes = w.nb * (b_gu + b_dn)
-    flops = 6.0 * D * I * float(w.nr.sum())
-    tok_s = T / (ms_step * 1e-3)
-    log(f"step {ms_step*1e3:.1f} us (wall {wall/args.steps*1e6:.1f} us): gate/up "
-        f"{ms_gu*1e3:.1f} us, down {ms_dn*1e3:.1f} us, combine {ms_cb*1e3:.1f} us; "
-        f"effective weight {wbytes/ms_step/1e6:.0f} GB/s")
-    gu_gbs = w.nb * b_gu / (ms_gu * 1e-3) / 1e9
-    dn_gbs = w.nb * b_dn / (ms_dn * 1e-3) / 1e9
-    log(f"gate/up {gu_gbs:.0f} GB/s, down {dn_gbs:.0f} GB/s")
+    cpu_s = 0.0 if args.no_cpu else args.cpu_seconds
+    head, pool, w = measure(np, torch, mvllm_hip, synth, args.config, T, args.steps,
+                            args.warmup, args.pool_gb, fp4act=args.fp4act, cpu_seconds=cpu_s)
 
     # achievable HBM streaming-read rate on this box: coalesced 16-byte loads over the
-    # whole pool (>= 4 GiB, beyond the Infinity Cache), after one warm-up pass
+    # headline's weight pool (beyond the Infinity Cache), after one warm-up pass; and a
+    # 1 GiB copy, whose known byte counts calibrate the FETCH_SIZE / WRITE_SIZE counters
     sink = torch.zeros(4096, dtype=torch.uint8, device="cuda")
-    probe_bytes = (pool.numel() // 4096) * 4096
-    hbm_gbs = probe_bytes / mvllm_hip.membench(0, pool, sink, probe_bytes, 0, 5) / 1e6
-    # copy probe (1 GiB read + 1 GiB written): with the read probe, the known byte counts
-    # that calibrate the FETCH_SIZE / WRITE_SIZE counters of a profiled run
+    probe_bytes = min((pool.pool.numel() // 4096) * 4096, 8 << 30)
+    hbm_gbs = probe_bytes / mvllm_hip.membench(0, pool.pool, sink, probe_bytes, 0, 5) / 1e6
     copy_bytes = min(1 << 30, probe_bytes)
     dst = torch.empty(copy_bytes, dtype=torch.uint8, device="cuda")
-    copy_gbs = 2 * copy_bytes / mvllm_hip.membench(1, pool, dst, copy_bytes, 0, 3) / 1e6
+    copy_gbs = 2 * copy_bytes / mvllm_hip.membench(1, pool.pool, dst, copy_bytes, 0, 3) / 1e6
     del dst
     log(f"HBM stream-read probe: {hbm_gbs:.0f} GB/s over {probe_bytes / 2**30:.2f} GiB; "
         f"copy probe {copy_gbs:.0f} GB/s (read + write) over {copy_bytes / 2**30:.2f} GiB")
-    sizes = {}
-    if args.probe_sizes:
-        flat = pool.view(-1)
-        for mib in (8, 16, 32, 64, 128, 192, 256, 512, 1024):
-            nb = mib << 20
-            if nb * 4 > probe_bytes:
-                break
-            ts, offset = [], 0
-            for r in range(20):
-                if offset + nb > probe_bytes:
-                    offset = 0
-                ms = mvllm_hip.membench(0, flat[offset:offset + nb], sink, nb, 0, 1)
-                offset += nb
-                if r >= 4:
-                    ts.append(ms)
-            t = float(np.median(ts))
-            sizes[mib] = {"us": round(t * 1e3, 2), "gbps": round(nb / t / 1e6, 1)}
-            log(f"  read {mib:5d} MiB in one launch: {t*1e3:8.2f} us, {nb / t / 1e6:7.0f} GB/s")
+    sizes = probe_sizes(np, mvllm_hip, pool.pool, sink, probe_bytes) if args.probe_sizes else {}
 
-    # the routing in front of the block on the device (moe_topk of every token, then the
-    # batched call's segments) for this layer shape, and its host counterpart
-    route, scores = route_timing(torch, mvllm_hip, T, E, k)
-    log(f"device routing (T={T}, E={E}, k={k}): {route['us_per_call']:.2f} us per call")
-
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, args.cpu_seconds)
-        route["cpu_us_per_call"], route["cpu_kind"] = cpu_route_baseline(np, scores, k)
-        log(f"host routing: {route['cpu_us_per_call']:.1f} us per call ({route['cpu_kind']})")
+    extra = {}
+    if not args.no_extra:
+        if args.config == "c4" and not args.fp4act:
+            rec, _, _ = measure(np, torch, mvllm_hip, synth, "c4", T, args.steps, 2,
+                                args.pool_gb, fp4act=True, pool=pool, w=w)
+            extra["c4 T=%d fp4act" % T] = rec
+        del pool
+        torch.cuda.empty_cache()
+        for name, t, steps in (("c3", 512, args.steps), ("c2", 1, 200), ("c1", 16, 200),
+                               ("c1", 4, 200), ("c1", 1, 200), ("c0", 1, 200)):
+            if (name, t) == (args.config, T):
+                continue
+            rec, p, _ = measure(np, torch, mvllm_hip, synth, name, t, steps, 20, args.pool_gb,
+                                cpu_seconds=0.0 if args.no_cpu else 3.0)
+            extra[f"{name} T={t}"] = rec
+            del p
+            torch.cuda.empty_cache()
+        extra["c2 T=1 staged"] = staged(args, np, torch, mvllm_hip, synth,
+                                        dict(synth.CONFIGS["c2"]), 1, 50, 5, 0.25, 0.0)
+        route, scores = route_timing(torch, mvllm_hip, 2048, 384, 8)
+        if not args.no_cpu:
+            route["cpu_us_per_call"], route["cpu_kind"] = cpu_route_baseline(np, scores, 8)
+        extra["route c4 shape"] = route
+    else:
+        del pool
 
     rec = {
-        "metric": "moe_block tokens/s (decode), effective weight GB/s",
-        "value": round(tok_s, 2),
-        "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 6),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": dtype,
+        "metric": METRIC, "value": head["value"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": head["dtype"],
         "data": "synthetic (seeded; weights random in the reference layouts, in a "
-                f"{n_blobs * nbytes / 2**30:.1f} GiB pool rotated per step)",
-        "config": {"workload": f"{args.config} {cfg['desc']}, T={T}", "D": D, "I": I, "E": E,
-                   "topk": k, "T": T, "fmt": fmt, "experts_per_step": int(w.nb),
-                   "rows": int(w.nr.sum()), "mode": args.mode, "fp4act": bool(args.fp4act),
-                   "options": args.opt},
-        "weight_gbps": round(wbytes / ms_step / 1e6, 1),
-        "hbm_probe_gbps": round(hbm_gbs, 1),
-        "hbm_copy_probe_gbps": round(copy_gbs, 1),
+                f"{head['pool_gib']:.1f} GiB pool; activations N(0,1) rounded to bf16)",
+        "config": {"workload": head["workload"], "D": cfg["D"], "I": cfg["I"], "E": cfg["E"],
+                   "topk": cfg["k"], "T": T, "fmt": cfg["fmt"], "routing": cfg["routing"],
+                   "experts_per_step": head["experts"], "rows": head["rows"],
+                   "mode": args.mode, "fp4act": bool(args.fp4act), "options": args.opt},
+        "weight_gbps": head["weight_gbps"], "mfma_util": head["mfma_util"],
+        "roofline": head["roofline"], "call_binding": head["call_binding"],
+        "phases_us": head["phases_us"], "kernel_sum_us": head["kernel_sum_us"],
+        "host_us_per_call": head["host_us_per_call"],
+        "hbm_probe_gbps": round(hbm_gbs, 1), "hbm_copy_probe_gbps": round(copy_gbs, 1),
         **({"hbm_probe_by_size_mib": sizes} if sizes else {}),
-        "mfma_util": round(flops / (ms_step * 1e-3) /
-                           ((FP4_PEAK_TFS if dtype == "mxfp4" else BF16_PEAK_TFS) * 1e12), 5),
-        "roofline": {"bound": "hbm", "kernel": "gate_up_gemv", "achieved": round(gu_gbs, 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_bytes(f"{args.config} T={T}", "gate_up"),
-                     "bytes_per_launch": int(w.nb * b_gu), "avg_launch_us": round(ms_gu * 1e3, 3)},
-        "phases_us": {"gate_up": round(ms_gu * 1e3, 3), "down": round(ms_dn * 1e3, 3),
-                      "combine": round(ms_cb * 1e3, 3)},
-        "cpu_baseline": cpu,
-        "route": route,
+        "cpu_baseline": head.get("cpu_baseline"),
+        "extra": extra,
     }
     print(json.dumps(rec), flush=True)
 
 
-def route_timing(torch, mvllm_hip, T, E, k, reps=200):
+def probe_sizes(np, mvllm_hip, pool, sink, probe_bytes):
+    """Stream-read probe at launch-sized reads; each size read 20 times at new offsets of
+    the pool (no Infinity Cache hits), median of the last 16."""
+    sizes, flat = {}, pool.view(-1)
+    for mib in (8, 16, 32, 64, 128, 192, 256, 512, 1024):
+        nb = mib << 20
+        if nb * 4 > probe_bytes:
+            break
+        ts, offset = [], 0
+        for r in range(20):
+            if offset + nb > probe_bytes:
+                offset = 0
+            ms = mvllm_hip.membench(0, flat[offset:offset + nb], sink, nb, 0, 1)
+            offset += nb
+            if r >= 4:
+                ts.append(ms)
+        t = float(np.median(ts))
+        sizes[mib] = {"us": round(t * 1e3, 2), "gbps": round(nb / t / 1e6, 1)}
+        log(f"  read {mib:5d} MiB in one launch: {t*1e3:8.2f} us, {nb / t / 1e6:7.0f} GB/s")
+    return sizes
+
+
+def route_timing(torch, mvllm_hip, T, E, k, reps=100):
     """GPU time per call of mvllm_hip_moe_route_dev (moe_topk of every token, then the
     segments) on N(0,1) router scores (weights from their sigmoid), HIP events on the
     null stream the calls are enqueued on.  Returns the record and the scores (for the
@@ -309,6 +375,7 @@ def route_timing(torch, mvllm_hip, T, E, k, reps=200):
     nb, n_rows = (int(v) for v in counts.cpu())
     rec = {"us_per_call": round(e0.elapsed_time(e1) / reps * 1e3, 3), "n_tok": T, "n_exp": E,
            "k": k, "experts": nb, "rows": n_rows, "launches_per_call": 5}
+    log(f"device routing (T={T}, E={E}, k={k}): {rec['us_per_call']:.2f} us per call")
     return rec, (choice.cpu().numpy(), mix.cpu().numpy())
 
 
@@ -331,10 +398,11 @@ def cpu_route_baseline(np, scores, k, budget_s=2.0):
         if time.perf_counter() - t0 > budget_s:
             break
     return round((time.perf_counter() - t0) / calls * 1e6, 1), \
-        f"{kind}; moe_topk per token through ctypes (~1 us call overhead each), then the segments"
+        f"{kind}; Python-driven: one ctypes call per token (~1 us of call overhead each), " \
+        "then the segments"
 
 
-def staged(args, np, torch, mvllm_hip, synth, cfg, T):
+def staged(args, np, torch, mvllm_hip, synth, cfg, T, steps, warmup, miss_rate, cpu_seconds):
     """One step = one drop-in mvllm_hip_moe_block call on host pointers (activations and
     output in host memory, as the engine calls it).  Expert blobs live in one pinned host
     buffer (the ExpertStore slots); most are promoted into the library's HBM tier at set-up,
@@ -343,10 +411,11 @@ def staged(args, np, torch, mvllm_hip, synth, cfg, T):
     compute.  Resident and host-only sets rotate over more than the Infinity Cache holds."""
     import ctypes
     D, I, fmt = cfg["D"], cfg["I"], cfg["fmt"]
-    w = synth.make_workload(args.config, T=T, with_experts=False)
+    name = [k for k, v in synth.CONFIGS.items() if v["desc"] == cfg["desc"]][0]
+    w = synth.make_workload(name, T=T, with_experts=False)
     nbytes, off = mvllm_hip.expert_geom(fmt, D, I)
     stride = (nbytes + 4095) // 4096 * 4096
-    n_miss = int(round(args.staged * w.nb))
+    n_miss = int(round(miss_rate * w.nb))
     n_res = w.nb - n_miss
     r_res = max(n_res, int(np.ceil(1.2 * 2**30 / nbytes)))   # resident blobs (> 1 GiB)
     r_host = max(n_miss, 2 * n_miss * 4)                      # host-only blobs
@@ -362,7 +431,7 @@ def staged(args, np, torch, mvllm_hip, synth, cfg, T):
     for b in range(r_res):
         mvllm_hip.promote(host + b * stride, nbytes, 0, b)
     torch.cuda.synchronize()
-    log(f"staged {args.config} T={T}: {w.nb} experts/step ({n_res} resident, {n_miss} misses), "
+    log(f"staged {name} T={T}: {w.nb} experts/step ({n_res} resident, {n_miss} misses), "
         f"{r_res} resident + {r_host} host-only blobs of {nbytes / 2**20:.2f} MiB")
     order = (0, 2, 4, 1, 3, 5)
 
@@ -382,87 +451,79 @@ def staged(args, np, torch, mvllm_hip, synth, cfg, T):
         mvllm_hip.moe_block(w.nb, D, I, fmt, *lists(s), w.xg, w.xoff, w.nr, w.rows, w.rw, out,
                             T, w.act, w.a, w.b)
 
-    for s in range(args.warmup):
+    for s in range(warmup):
         step(s)
     mvllm_hip.set_option("timing", 1)
     mvllm_hip.stats_reset()
     t0 = time.perf_counter()
-    for s in range(args.steps):
-        step(args.warmup + s)
-    wall = (time.perf_counter() - t0) / args.steps
+    for s in range(steps):
+        step(warmup + s)
+    wall = (time.perf_counter() - t0) / steps
     st = mvllm_hip.stats()
     mvllm_hip.set_option("timing", 0)
-    ms_gu, ms_dn = st["ms_gate_up"] / args.steps, st["ms_down"] / args.steps
-    h2d = st["h2d_weight_bytes"] / args.steps
-    log(f"step {wall * 1e6:.1f} us: misses/step {st['misses'] / args.steps:.1f}, "
-        f"hits/step {st['resident_hits'] / args.steps:.1f}, staged {h2d / 2**20:.1f} MiB/step "
-        f"({h2d / wall / 1e9:.1f} GB/s over the step); gate/up {ms_gu * 1e3:.1f} us, "
-        f"down {ms_dn * 1e3:.1f} us (HIP events, compute stream)")
-    gq, sb = (64, 4) if fmt == 4 else (32, 1)
-    b_gu = 2 * (I * (D // 2) + I * ((D + gq - 1) // gq) * sb)
+    ms_gu, ms_dn = st["ms_gate_up"] / steps, st["ms_down"] / steps
+    h2d = st["h2d_weight_bytes"] / steps
+    log(f"[{name} T={T} staged] step {wall * 1e6:.1f} us: misses/step "
+        f"{st['misses'] / steps:.1f}, hits/step {st['resident_hits'] / steps:.1f}, staged "
+        f"{h2d / 2**20:.1f} MiB/step ({h2d / wall / 1e9:.1f} GB/s over the step); gate/up "
+        f"{ms_gu * 1e3:.1f} us, down {ms_dn * 1e3:.1f} us (HIP events, compute stream)")
+    b_gu, _ = expert_bytes(fmt, D, I)
     gu_gbs = w.nb * b_gu / (ms_gu * 1e-3) / 1e9
-    cpu = None
-    if not args.no_cpu:
-        cpu = cpu_baseline(np, torch, w, pool, pstride, poff, fmt, D, I, T, args.cpu_seconds)
     rec = {
-        "metric": "moe_block tokens/s (decode), effective weight GB/s",
-        "value": round(T / wall, 3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(wall * 1e3, 6), "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "bf16x2",
-        "data": "synthetic (seeded; weights random in the reference layouts, pinned host slots)",
-        "config": {"workload": f"{args.config} {cfg['desc']}, T={T}, drop-in host entry, "
-                               f"{n_miss} of {w.nb} experts staged from pinned host memory",
-                   "D": D, "I": I, "E": cfg["E"], "topk": cfg["k"], "T": T, "fmt": fmt,
-                   "miss_rate": args.staged, "includes": "PCIe H2D of misses, xg and out"},
+        "workload": f"{name} {cfg['desc']}, T={T}, drop-in host entry, {n_miss} of {w.nb} "
+                    "experts staged from pinned host memory",
+        "value": round(T / wall, 3), "unit": "tokens/s", "ms_per_step": round(wall * 1e3, 6),
+        "dtype": "bf16x2", "miss_rate": miss_rate,
+        "includes": "PCIe H2D of misses, xg and out; the call's final wait",
         "staged_mib_per_step": round(h2d / 2**20, 2),
+        "host_us_per_call": round(st["host_ms"] / steps * 1e3, 1),
         "roofline": {"bound": "hbm", "kernel": "gate_up (resident + staged experts)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": cpu,
     }
-    print(json.dumps(rec), flush=True)
+    if cpu_seconds > 0:
+        rec["cpu_baseline"] = cpu_baseline(np, torch, w, pool, pstride, poff, fmt, D, I, T,
+                                           cpu_seconds)
+    for b in range(r_res):
+        mvllm_hip.evict(0, b)
+    L.mvllm_hip_host_free(host)
+    del pool
+    torch.cuda.empty_cache()
+    return rec
 
 
 def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):
     """The reference's host moe_block (oracle/_ref build when present, else the C
     restatement) on layer 0's experts, single thread, bounded to ~budget_s.  Decode
-    workloads run whole calls; when one call would take far longer than the budget
-    (prefill), experts are run one per call (as the engine calls moe_block, nb=1) in
-    segment order until the budget is spent, and the full call is extrapolated by MACs."""
+    workloads run whole calls (median of at least 5 when they fit the budget); when one
+    call would take far longer than the budget (prefill), experts are run one per call (as
+    the engine calls moe_block, nb=1) in segment order until the budget is spent, and the
+    full call is extrapolated by MACs."""
     import oracle
     kind = "reference" if oracle.have_ref() else "port"
     cpu = oracle.CpuMoe("ref" if kind == "reference" else "oracle")
-    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+    from mvllm_hip import synth
     macs_e = [3.0 * D * I * int(n) for n in w.nr]
     macs_total = float(sum(macs_e))
 
     def expert(i):
-        host = pool[i].cpu().numpy()
-
-        def piece(oi, O, K, scale):
-            o = int(off[oi])
-            if scale:
-                n = O * ((K + gq - 1) // gq)
-                return host[o:o + n * sb].view(np.float32 if fmt == 4 else np.uint8).reshape(O, -1)
-            return host[o:o + O * ((K + 1) // 2)].reshape(O, -1)
-        return (piece(0, I, D, False), piece(2, I, D, False), piece(4, D, I, False),
-                piece(1, I, D, True), piece(3, I, D, True), piece(5, D, I, True))
+        return synth.blob_pieces(pool[i].cpu().numpy(), fmt, D, I, off)
 
     if macs_total / 1e9 <= 4 * budget_s:  # whole calls (about 1 GMAC/s on one core)
         ex = [expert(i) for i in range(w.nb)]
         lists = [[e[k] for e in ex] for k in range(6)]
-        calls, t0 = 0, time.perf_counter()
+        ts, t_all = [], time.perf_counter()
         while True:
             o = np.zeros((T, D), np.float32)
+            t0 = time.perf_counter()
             cpu.moe_block(w.nb, D, I, fmt, *lists, w.xg, w.xoff, w.nr, w.rows, w.rw, o, T,
                           w.act, w.a, w.b)
-            calls += 1
-            el = time.perf_counter() - t0
-            if el >= budget_s or calls >= 50:
+            ts.append(time.perf_counter() - t0)
+            if (time.perf_counter() - t_all >= budget_s and len(ts) >= 5) or len(ts) >= 50:
                 break
-        per = el / calls
-        sample = (f"{calls} full moe_block calls of the same workload (T={T}, {w.nb} experts) "
-                  f"in {el:.1f} s, single-threaded host code")
+        per = float(np.median(ts))
+        sample = (f"median of {len(ts)} full moe_block calls of the same workload (T={T}, "
+                  f"{w.nb} experts), single-threaded host code")
     else:
         o = np.zeros((T, D), np.float32)
         done, el, n_e = 0.0, 0.0, 0

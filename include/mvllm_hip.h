@@ -226,8 +226,10 @@ void *mvllm_hip_resident_ptr(int layer, int eid);
  *     MXFP4 quantization of x and of H)
  *  13 launches gate/up    14 launches down
  *  15 host ms spent inside the moe_block entry points (plan building, argument
- *     marshalling and launches; for mvllm_hip_moe_block also the copies and the wait)
- *  16 reserved (0)
+ *     marshalling and launches; for mvllm_hip_moe_block also the copies and the wait),
+ *     including 16
+ *  16 host ms of 15 spent blocked until the device finished earlier calls whose pinned
+ *     plan slots are reused (a host running ahead of the device waits there)
  * Kernel times are filled only with option "timing"=1.  Returns the count written
  * (<= n). */
 int mvllm_hip_stats(double *vals, int n);

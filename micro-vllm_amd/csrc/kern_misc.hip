@@ -9,7 +9,10 @@ namespace mvllm_hip {
 // row order), each step rounded as `orow[i] += w * hr[i]` rounds on the host
 // (src/gpu/metal_ops.cpp:328-339): a product, then a sum, no fused multiply-add.
 // The entries' loads are issued in batches of 8 before the ordered accumulation.
+// Contraction is off here, for the operators written in this function: clang would
+// otherwise fuse the product and the sum into one v_fmac, which rounds once.
 __global__ __launch_bounds__(64) void k_combine(CombineArgs A) {
+#pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int e0 = A.tok_ptr[t], e1 = A.tok_ptr[t + 1];
     float *orow = A.out + (size_t)A.out_row[t] * (size_t)A.D;
@@ -32,10 +35,10 @@ __global__ __launch_bounds__(64) void k_combine(CombineArgs A) {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 if (eb + i < e1) {
-                    o.x = __fadd_rn(o.x, __fmul_rn(w[i], y[i].x));
-                    o.y = __fadd_rn(o.y, __fmul_rn(w[i], y[i].y));
-                    o.z = __fadd_rn(o.z, __fmul_rn(w[i], y[i].z));
-                    o.w = __fadd_rn(o.w, __fmul_rn(w[i], y[i].w));
+                    o.x = o.x + w[i] * y[i].x;
+                    o.y = o.y + w[i] * y[i].y;
+                    o.z = o.z + w[i] * y[i].z;
+                    o.w = o.w + w[i] * y[i].w;
                 }
             }
         }
@@ -45,7 +48,7 @@ __global__ __launch_bounds__(64) void k_combine(CombineArgs A) {
              d += 64) {
             float o = orow[d];
             for (int e = e0; e < e1; ++e)
-                o = __fadd_rn(o, __fmul_rn(A.ent_w[e], A.Y[(size_t)A.ent_row[e] * A.D + d]));
+                o = o + A.ent_w[e] * A.Y[(size_t)A.ent_row[e] * A.D + d];
             orow[d] = o;
         }
     }

@@ -252,7 +252,15 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
     P = Plan();
     P.D = D;
     P.I = Iinter;
-    int base = 0;
+    size_t total = 0;
+    for (int e = 0; e < nb; ++e)
+        total += nr[e] > 0 ? (size_t)nr[e] : 0;
+    P.xrow.reserve(total);
+    P.dest.reserve(total);
+    P.w.reserve(total);
+    P.ew.reserve(nb);
+    P.src_expert.reserve(nb);
+    int base = 0, max_dest = -1;
     for (int e = 0; e < nb; ++e) {
         const int nre = nr[e];
         if (nre <= 0)
@@ -278,6 +286,7 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
                 P.xrow.push_back(xoff[e] + r);
                 P.dest.push_back(dst);
                 P.w.push_back(rw[base + r]);
+                max_dest = std::max(max_dest, dst);
             }
             w.nrows = static_cast<int>(P.xrow.size()) - w.row0;
             if (w.nrows > 0) {
@@ -288,21 +297,44 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
         }
         base += nre;
     }
-    // combine CSR over destination tokens (ascending), entries in compact-row order
+    // Combine CSR over destination rows (ascending), each row's entries in compact-row
+    // (= expert) order: a stable counting sort by destination (a comparison sort of the
+    // rows took 1.2 ms per call at 16,384 rows); destinations spread far beyond the row
+    // count (host entry with S <= 0) take the comparison sort.
     const int R = static_cast<int>(P.dest.size());
-    std::vector<int> order(R);
-    for (int j = 0; j < R; ++j)
-        order[j] = j;
-    std::stable_sort(order.begin(), order.end(),
-                     [&](int a, int b) { return P.dest[a] < P.dest[b]; });
-    for (int i = 0; i < R; ++i) {
-        const int j = order[i];
-        if (i == 0 || P.dest[j] != P.dest[order[i - 1]]) {
-            P.tok_ptr.push_back(i);
-            P.out_row.push_back(P.dest[j]);
+    P.ent_row.resize(R);
+    P.ent_w.resize(R);
+    if ((size_t)max_dest + 1 <= 4 * (size_t)R + 4096) {
+        std::vector<int> pos((size_t)max_dest + 2, 0);
+        for (int j = 0; j < R; ++j)
+            ++pos[(size_t)P.dest[j] + 1];
+        for (int t = 0; t <= max_dest; ++t) {
+            if (pos[(size_t)t + 1]) {
+                P.tok_ptr.push_back(pos[t]);
+                P.out_row.push_back(t);
+            }
+            pos[(size_t)t + 1] += pos[t];
         }
-        P.ent_row.push_back(j);
-        P.ent_w.push_back(P.w[j]);
+        for (int j = 0; j < R; ++j) {
+            const int at = pos[P.dest[j]]++;
+            P.ent_row[at] = j;
+            P.ent_w[at] = P.w[j];
+        }
+    } else {
+        std::vector<int> order(R);
+        for (int j = 0; j < R; ++j)
+            order[j] = j;
+        std::stable_sort(order.begin(), order.end(),
+                         [&](int a, int b) { return P.dest[a] < P.dest[b]; });
+        for (int i = 0; i < R; ++i) {
+            const int j = order[i];
+            if (i == 0 || P.dest[j] != P.dest[order[i - 1]]) {
+                P.tok_ptr.push_back(i);
+                P.out_row.push_back(P.dest[j]);
+            }
+            P.ent_row[i] = j;
+            P.ent_w[i] = P.w[j];
+        }
     }
     P.tok_ptr.push_back(R);
 }
@@ -636,8 +668,13 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     PlanSlot &s = C.slots[si];
     C.slot_next = (si + 1) % Ctx::kSlots;
     const int gi = si / Ctx::kGroup;
-    if (si % Ctx::kGroup == 0 && C.grp_used[gi])
-        HIP_TRY(hipEventSynchronize(C.grp_done[gi]));  // the group's previous calls are done
+    if (si % Ctx::kGroup == 0 && C.grp_used[gi]) {
+        // the group's previous calls are done (time blocked here: stats[16])
+        const auto t0 = std::chrono::steady_clock::now();
+        HIP_TRY(hipEventSynchronize(C.grp_done[gi]));
+        C.stats[16] += std::chrono::duration<double, std::milli>(
+                           std::chrono::steady_clock::now() - t0).count();
+    }
     if (si % Ctx::kGroup == Ctx::kGroup - 1)
         C.open_last = si;
     auto al = [](size_t n) { return (n + 255) & ~size_t(255); };

@@ -84,6 +84,45 @@ def make_expert(rng, fmt, D, I):
     return ex
 
 
+def device_pool(torch, fmt, D, I, n_blobs, seed, geom):
+    """n_blobs expert blobs in the reference layout, generated on the GPU with the same
+    distributions as make_expert (codes uniform over all bytes; int4 scales U(0.005, 0.02)
+    rounded to bf16 and stored as f32; ue8m0 bytes in [118, 124]).  geom = expert_geom's
+    (bytes, offsets[6]).  Returns (pool [n_blobs, stride] uint8 on the device, stride)."""
+    nbytes, off = geom
+    stride = (nbytes + 255) // 256 * 256
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    pool = torch.randint(0, 256, (n_blobs, stride), dtype=torch.uint8, device="cuda",
+                         generator=g)
+    gq = 64 if fmt == 4 else 32
+    for oi, O, K in ((1, I, D), (3, I, D), (5, D, I)):  # scale pieces: (offset index, O, K)
+        ns = O * ((K + gq - 1) // gq)
+        o = int(off[oi])
+        if fmt == 4:
+            s = torch.empty((n_blobs, ns), dtype=torch.float32, device="cuda")
+            s.uniform_(0.005, 0.02, generator=g)
+            s = s.to(torch.bfloat16).to(torch.float32)  # bf16-valued scales stored as f32
+            pool[:, o:o + 4 * ns] = s.view(torch.uint8).view(n_blobs, 4 * ns)
+        else:
+            pool[:, o:o + ns] = torch.randint(118, 125, (n_blobs, ns), dtype=torch.uint8,
+                                              device="cuda", generator=g)
+    return pool, stride
+
+
+def blob_pieces(blob, fmt, D, I, off):
+    """Host numpy views (gp, up, dp, gs, us, ds) of one expert blob (uint8 numpy)."""
+    gq, sb = (64, 4) if fmt == 4 else (32, 1)
+
+    def piece(oi, O, K, scale):
+        o = int(off[oi])
+        if scale:
+            n = O * ((K + gq - 1) // gq)
+            return blob[o:o + n * sb].view(np.float32 if fmt == 4 else np.uint8).reshape(O, -1)
+        return blob[o:o + O * ((K + 1) // 2)].reshape(O, -1)
+    return (piece(0, I, D, False), piece(2, I, D, False), piece(4, D, I, False),
+            piece(1, I, D, True), piece(3, I, D, True), piece(5, D, I, True))
+
+
 @dataclass
 class Workload:
     name: str
