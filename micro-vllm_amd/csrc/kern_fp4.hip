@@ -38,6 +38,7 @@ struct F4Args {
     float *hout;            // dual: H f32 [rcap][O]
     float *out;             // single: Y f32 [rcap][O]
     int nbn, K, O, rcap;
+    int xcd;  // 1: tasks ordered per XCD (xcd_task)
     int act;
     float act_a, act_b;
 };
@@ -64,8 +65,10 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int PA = MT >= 8 ? 1 : 2;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    const int item = blockIdx.x / A.nbn;
-    const int nb = blockIdx.x - item * A.nbn;
+    const int n_tasks = (int)gridDim.x;
+    const int task = A.xcd ? xcd_task(blockIdx.x, n_tasks) : (int)blockIdx.x;
+    const int item = task / A.nbn;
+    const int nb = task - item * A.nbn;
     const F4Item it = A.items[item];
     const ExpertWork &ew = A.ew[it.a];
     const int K = A.K, O = A.O, nrow = it.nrow;
@@ -166,7 +169,8 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     };
 
     // pipeline as the bf16 grouped GEMM (weights two steps ahead, activations staged one
-    // step ahead from registers loaded PA steps ahead; no branches around the loads)
+    // step ahead from registers loaded PA steps ahead; no branches around the loads;
+    // prefetches past the last step read that step again)
     const int nk = K / 256;
     F4Step b0, b1;
     AStage ra0, ra1;
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     if constexpr (PA == 2)
         load_a(ra1, min(1, nk - 1));
     load_b(b0, 0);
-    load_b(b1, 1);
+    load_b(b1, min(1, nk - 1));
     store_a(ra0, 0);
     __syncthreads();
     for (int k = 0; k < nk; k += 2) {
@@ -184,7 +188,7 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             load_a(ra1, min(k + 1, nk - 1));
         compute(b0, 0);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, k + 2);
+        load_b(b0, min(k + 2, nk - 1));  // past the end: the last step again (L2 hits)
         store_a(ra1, 1);
         __syncthreads();
         if (k + 1 >= nk)
@@ -195,7 +199,7 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             load_a(ra0, min(k + 2, nk - 1));
         compute(b1, 1);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, k + 3);
+        load_b(b1, min(k + 3, nk - 1));
         store_a(ra0, 0);
         __syncthreads();
     }
@@ -247,6 +251,7 @@ hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *
     a.hout = hout;
     a.out = out;
     a.nbn = O / (dual ? 128 : 256);
+    a.xcd = gemm_xcd() ? 1 : 0;
     a.K = K;
     a.O = O;
     a.rcap = rcap;

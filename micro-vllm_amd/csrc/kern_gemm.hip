@@ -43,6 +43,7 @@ struct GemmArgs {
     float *out;         // single: Y [rcap][O] f32
     int nbn;            // column blocks per item
     int n_tasks;        // items * nbn
+    int xcd;            // 1: tasks ordered per XCD (xcd_task), 0: task = workgroup index
     int K, O, rcap;
     int act;
     float act_a, act_b;
@@ -328,9 +329,9 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // harmless bytes that are never consumed, so the body has no branches around its
     // loads; the scheduling barriers keep each step's uses of a register set ahead of the
     // loads that refill it.
-    const int task = blockIdx.x;
-    if (task >= n_tasks)
+    if ((int)blockIdx.x >= n_tasks)
         return;
+    const int task = A.xcd ? xcd_task(blockIdx.x, n_tasks) : (int)blockIdx.x;
     const TaskD<FMT> cur = make_task(task);
     GStep<FMT> b0, b1;
     GScale<FMT> sc, sn;  // scales of this pair of steps / of the next pair
@@ -345,41 +346,39 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (PA == 2)
             load_a(ra1, cur, min(1, nk - 1));
-        load_b(b1, cur, 1);
+        load_b(b1, cur, min(1, nk - 1));
         __builtin_amdgcn_sched_barrier(0);
         store_a(ra0, 0);
         __syncthreads();
     };
     // Even step k: LDS buffer 0, weights b0; stages A(k + 1) into buffer 1.  Prefetches
-    // past the task's last step wrap to its first steps (harmless bytes).
+    // past the task's last step read its last step again (L2 hits, never consumed):
+    // wrapping to the first steps instead re-read two steps of weights from HBM per task,
+    // a quarter of the bytes at K = 2048.
     auto step_even = [&] __attribute__((always_inline)) (int k, auto exact) {
-        const bool tail = k + 2 >= nk;
-        const TaskD<FMT> &pd = cur;
-        const int k2 = tail ? k + 2 - nk : k + 2;
+        const int k2 = min(k + 2, nk - 1);
         sc = sn;
         if constexpr (PA == 2)
-            load_a(ra0, pd, min(k2, nk - 1));
+            load_a(ra0, cur, k2);
         else
             load_a(ra1, cur, min(k + 1, nk - 1));
         compute(b0, 0, sc, 0, exact);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, pd, k2);
-        load_s(sn, pd, k2);
+        load_b(b0, cur, k2);
+        load_s(sn, cur, k2);
         store_a(ra1, 1);
         __syncthreads();
     };
     // odd step k + 1: LDS buffer 1, weights b1; stages A(k + 2) into buffer 0
     auto step_odd = [&] __attribute__((always_inline)) (int k, auto exact) {
-        const bool tail = k + 2 >= nk;
-        const TaskD<FMT> &pd = cur;
-        const int k2 = tail ? k + 2 - nk : k + 2;
+        const int k3 = min(k + 3, nk - 1);
         if constexpr (PA == 2)
-            load_a(ra1, pd, min(k2 + 1, nk - 1));
+            load_a(ra1, cur, k3);
         else
-            load_a(ra0, pd, min(k2, nk - 1));
+            load_a(ra0, cur, min(k + 2, nk - 1));
         compute(b1, 1, sc, 1, exact);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, pd, k2 + 1);
+        load_b(b1, cur, k3);
         store_a(ra0, 0);
         __syncthreads();
     };
@@ -461,6 +460,10 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
 
 // ---- launchers ----------------------------------------------------------------------
 
+static bool g_gemm_xcd = true;  // option "gemm_xcd"
+void gemm_set_xcd(bool on) { g_gemm_xcd = on; }
+bool gemm_xcd() { return g_gemm_xcd; }
+
 template <int FMT, bool DUAL, int TERMS, int MT>
 static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
     const size_t lds = gemm_lds_bytes(FMT, TERMS, MT);
@@ -474,6 +477,7 @@ static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
         attr = true;
     }
     a.n_tasks = n_items * a.nbn;
+    a.xcd = g_gemm_xcd ? 1 : 0;
     hipLaunchKernelGGL(kern, dim3((unsigned)a.n_tasks), dim3(kGemmThreads), lds, st, a);
     return hipGetLastError();
 }

@@ -145,6 +145,15 @@ __device__ __forceinline__ float split_terms(float x, __bf16 (&t)[3]) {
     return rep;
 }
 
+// Task of workgroup b out of n when the dispatcher hands workgroups to the 8 XCDs in
+// turn (b % 8): XCD x runs the contiguous task range starting at x * n / 8 (the first
+// n % 8 XCDs one task more), so consecutive tasks -- the column blocks of one item, and
+// the row blocks of one expert -- share that XCD's L2 and are dispatched together.
+__device__ __forceinline__ int xcd_task(int b, int n) {
+    const int q = n >> 3, r = n & 7, x = b & 7, s = b >> 3;
+    return x < r ? x * (q + 1) + s : r * (q + 1) + (x - r) * q + s;
+}
+
 // Raw buffer resource over [p, p + bytes) (gfx9 descriptor: stride 0, word 3 = 0x20000).
 // Loads through it take a per-lane 32-bit offset plus a wave-uniform offset; offsets past
 // `bytes` read as 0.

@@ -151,6 +151,10 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
 // expert's weights fewer times; MT = 8 spills at most 5 registers.
 inline int gemm_max_mt(int fmt, int terms) { return (void)fmt, terms == 1 ? 8 : 4; }
 size_t gemm_lds_bytes(int fmt, int terms, int mt);
+// Grouped-GEMM task order (option "gemm_xcd"): 1 (default) = each XCD runs a contiguous
+// range of tasks (an item's column blocks share one L2), 0 = task = workgroup index.
+void gemm_set_xcd(bool on);
+bool gemm_xcd();
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act, float act_a, float act_b,

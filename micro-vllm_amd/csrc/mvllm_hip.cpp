@@ -1207,6 +1207,8 @@ int mvllm_hip_set_option(const char *key, long long value) {
         if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8)
             return 0;
         C.dec_ks = static_cast<int>(value);
+    } else if (k == "gemm_xcd") {
+        gemm_set_xcd(value != 0);
     } else if (k == "dec_inline") {
         C.dec_inline = value ? 1 : 0;
     } else if (k == "combine_ordered") {

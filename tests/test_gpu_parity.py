@@ -477,6 +477,23 @@ def test_gemm_parity(hip, case, mode, tol):
             assert np.array_equal(got[t], c.out[t])
 
 
+@pytest.mark.parametrize("case", [GEMM_CASES[0], GEMM_CASES[3], GEMM_CASES[4]])
+def test_gemm_task_order(hip, case):
+    """Option gemm_xcd only reorders the tasks over the XCDs: every output element comes
+    from the same tile and the same summation, so results are bit-identical."""
+    fmt, D, I, nr, S, act, a, b, nulls, bad = case
+    say("gemm task order", case)
+    rng = np.random.default_rng(D * 17 + I + sum(nr))
+    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
+    base = _gemm_run(hip, c, 0)
+    assert hip.set_option("gemm_xcd", 0)
+    try:
+        other = _gemm_run(hip, c, 0)
+    finally:
+        hip.set_option("gemm_xcd", 1)
+    assert np.array_equal(base.view(np.uint32), other.view(np.uint32))
+
+
 @pytest.mark.parametrize("fmt,D,I,nr,act,a,b", [
     (4, 6144, 2048, [40, 21, 1], 1, 7.0, 0.0),          # c3 shapes
     (7, 7168, 2048, [130, 3, 17], 2, 4.0, 25.0),         # c4 shapes, a full 128-row block
