@@ -244,6 +244,16 @@ void mvllm_hip_stats_reset(void);
 int mvllm_hip_dequant(int fmt, const void *packed_dev, const void *scales_dev, int O, int K,
                       float *w_dev);
 
+/* The bf16 planes the matrix-core paths feed from f32 rows, exactly as the device forms
+ * them (the same conversion, split_terms, serves the decode kernels' activations and H):
+ * x_dev [n, K] f32 -> planes_dev [terms][n][K] bf16 bit patterns (uint16), plane 0 =
+ * bf16_round(x) (src/quant/bf16.cpp:9-20, round to nearest even), plane 1 = bf16_round of
+ * x - plane 0 (0 when plane 0 is not finite), plane 2 = the next remainder.  fmt 4 stores
+ * each 8-element block in the int4 operand order (elements 0 2 4 6 1 3 5 7), fmt 7 in
+ * natural order.  terms 1..3, K a multiple of 8.  Synchronous.  1 ok. */
+int mvllm_hip_bf16_planes(int fmt, int terms, const float *x_dev, int n, int K,
+                          uint16_t *planes_dev);
+
 /* MXFP4 activation quantization on the device, bit-exact with fp4_activation_qdq
  * (src/quant/native_act.cpp:159-179) for block 32: rows x [n, K] f32 ->
  * codes [n, K/2] packed e2m1 (low nibble = even k) + scales [n, K/32] ue8m0.

@@ -1669,6 +1669,21 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
     return 1;
 }
 
+int mvllm_hip_bf16_planes(int fmt, int terms, const float *x_dev, int n, int K,
+                          uint16_t *planes_dev) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !x_dev || !planes_dev || (fmt != 4 && fmt != 7) || terms < 1 ||
+        terms > 3 || n < 1 || K < 8 || K % 8) {
+        set_err("bf16_planes: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_prep_planes(fmt, terms, x_dev, nullptr, n, K, n, planes_dev, C.own));
+    HIP_TRY(hipStreamSynchronize(C.own));
+    return 1;
+}
+
 int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
                              uint8_t *scales_dev) {
     Ctx &C = ctx();

@@ -58,6 +58,7 @@ _SIGS = {
     "mvllm_hip_stats_reset": (None, []),
     "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
     "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
+    "mvllm_hip_bf16_planes": (_i, [_i, _i, _p, _i, _i, _p]),
     "mvllm_hip_moe_topk_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "mvllm_hip_moe_segments_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p,
                                         _p]),
@@ -258,6 +259,11 @@ def moe_route_dev(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, r
                                          _ptr(wt), _ptr(work), _ptr(eids), _ptr(xoff), _ptr(nr),
                                          _ptr(rows), _ptr(rw), len(eids), len(rows), _ptr(counts),
                                          _stream(stream)), "mvllm_hip_moe_route_dev")
+
+
+def bf16_planes(fmt, terms, x_dev, n, K, planes_dev):
+    _check(lib().mvllm_hip_bf16_planes(fmt, terms, _ptr(x_dev), n, K, _ptr(planes_dev)),
+           "mvllm_hip_bf16_planes")
 
 
 def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):

@@ -92,7 +92,8 @@ class CpuMoe:
             L.ref_fp4_activation_qdq.argtypes = [_p, _p, _p, _i, _i]
             for name, args in {"quantize_int4_g64": [_p, _i, _i, _p, _p],
                                "pack_mxfp4": [_p, _i, _i, _p, _p],
-                               "silu_mul": [_p, _p, _i]}.items():
+                               "silu_mul": [_p, _p, _i],
+                               "bf16_round_array": [_p, _i]}.items():
                 fn = getattr(L, f"ref_{name}")
                 fn.restype, fn.argtypes = None, args
 
@@ -111,6 +112,13 @@ class CpuMoe:
 
     def bf16_round(self, v):
         return self.fn("bf16_round")(v)
+
+    def bf16_round_array(self, x):
+        """The reference's bf16_round_array (src/quant/bf16.cpp:36-41) on a copy of x
+        (f32 bit patterns pass through unchanged, NaN payloads included); _ref only."""
+        a = np.array(x, dtype=np.float32, copy=True)
+        self.lib.ref_bf16_round_array(a.ctypes.data, a.size)
+        return a
 
     # ---- GEMMs ---------------------------------------------------------------
     def matmul(self, fmt, x, w, scales=None):

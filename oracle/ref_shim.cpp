@@ -59,6 +59,7 @@ int ref_moe_union_ids(const int *idx, int n_tok, int topk, int *out, int cap) {
 }
 
 float ref_bf16_round(float v) { return bf16_round(v); }
+void ref_bf16_round_array(float *v, int n) { bf16_round_array(v, n); }
 float ref_e8m0_decode(uint8_t v) { return e8m0_decode(v); }
 float ref_e2m1_decode(uint8_t v) { return e2m1_decode(v); }
 int ref_fp4_activation_qdq(float *o, uint8_t *s, const float *in, int len, int bs) {

@@ -133,6 +133,51 @@ def test_quantize_mxfp4_bit_exact(hip, orc):
         assert np.array_equal(npref.unpack_nibbles(cg[r:r + 1], K)[0], cd), r
 
 
+@pytest.mark.parametrize("fmt", [4, 7])
+def test_bf16_planes_bit_exact(hip, fmt):
+    """The device's bf16 activation terms against the reference's bf16_round
+    (src/quant/bf16.cpp:9-20), through mvllm_hip.synth.bf16_round, which the CPU suite pins
+    to the reference build bit for bit.  The same conversion (split_terms) feeds the
+    grouped GEMM's planes, the decode kernels' activations and H.  Every term count:
+    plane 0 = bf16_round(x), plane 1 = bf16_round(x - plane 0) (0 for non-finite plane 0),
+    plane 2 = bf16_round of the next remainder.  Values: random magnitudes over the whole
+    exponent range, exact ties (even and odd), subnormals, +-0, +-Inf and quiet NaN.  A NaN
+    whose payload lies only in the low 16 bits is left out: the reference truncates it to
+    Inf, the device's converter keeps it a NaN (no bf16_round'ed input is such a NaN)."""
+    from mvllm_hip import synth
+    say("bf16 planes", fmt)
+    rng = np.random.default_rng(41 + fmt)
+    n, K = 8, 512
+    hi = rng.integers(0, 1 << 16, size=n * K, dtype=np.uint32)
+    lo = rng.choice(np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32), size=n * K)
+    bits = (hi << 16) | lo
+    bits[:8] = [0x00000000, 0x80000000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x00008000,
+                0x00018000, 0x807F8000]
+    expo_all_ones = (bits & 0x7F800000) == 0x7F800000
+    low_only_nan = expo_all_ones & ((bits & 0x007F0000) == 0) & ((bits & 0xFFFF) != 0)
+    bits[low_only_nan] = 0x7FC00000
+    x = bits.view(np.float32).reshape(n, K)
+    # element e of an 8-block is stored at a_slot(e): int4 order 0 2 4 6 1 3 5 7
+    slot = np.array([0, 4, 1, 5, 2, 6, 3, 7]) if fmt == 4 else np.arange(8)
+    for terms in (1, 2, 3):
+        planes = torch.zeros((terms, n, K), dtype=torch.int16, device="cuda")
+        hip.bf16_planes(fmt, terms, dev(x), n, K, planes)
+        got = planes.cpu().numpy().view(np.uint16).reshape(terms, n, K // 8, 8)
+        got = got[..., slot].reshape(terms, n, K)
+        rem = x.copy()
+        for tm in range(terms):
+            exp = synth.bf16_round(rem)
+            eb = (exp.view(np.uint32) >> 16).astype(np.uint16)
+            nan = np.isnan(exp)
+            got_nan = ((got[tm] & 0x7F80) == 0x7F80) & ((got[tm] & 0x7F) != 0)
+            assert np.array_equal(got_nan, nan), (terms, tm)
+            ok = got[tm][~nan] == eb[~nan]
+            assert ok.all(), (terms, tm, np.nonzero(~ok)[0][:5])
+            with np.errstate(invalid="ignore"):
+                nxt = (rem - exp).astype(np.float32)
+            rem = np.where(np.isfinite(exp), nxt, np.float32(0)).astype(np.float32)
+
+
 # ------------------------------------------------------------- f32 GEMV parity
 
 DEV_CASES = [

@@ -280,6 +280,26 @@ def _bits(a):
     return np.asarray(a, np.float32).view(np.uint32)
 
 
+def test_synth_bf16_round_matches_ref(ref):
+    """The product's own bf16 rounding of inputs (mvllm_hip.synth.bf16_round) equals the
+    reference's bf16_round (src/quant/bf16.cpp:9-20) bit for bit over every high half with
+    low halves that hit each rounding case: zero, just below / at / just above the tie,
+    odd and even high halves (ties to even), subnormals, +-0, +-Inf, and NaNs whose
+    payload lies in the low half only (truncated to +-Inf by the reference) or in both.
+    Plus the reference's KATs (tests/test_host.cpp:8479-8483)."""
+    from mvllm_hip import synth
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xC000, 0xFFFF], np.uint32)
+    bits = (hi[:, None] | lows[None, :]).ravel()
+    x = bits.view(np.float32)
+    got = synth.bf16_round(x).view(np.uint32)
+    exp = ref.bf16_round_array(x).view(np.uint32)
+    bad = np.nonzero(got != exp)[0]
+    assert bad.size == 0, [(hex(bits[i]), hex(got[i]), hex(exp[i])) for i in bad[:5]]
+    assert synth.bf16_round(np.float32([1.00390625]))[0] == 1.0
+    assert synth.bf16_round(np.float32([1.01171875]))[0] == 1.015625
+
+
 def test_ref_scalars_bit_exact(orc, ref):
     rng = np.random.default_rng(21)
     vals = np.concatenate([rng.standard_normal(2000) * 10, [0.0, -0.0, 88.0, -88.0, 1e-30, 30.0,
