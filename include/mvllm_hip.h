@@ -134,8 +134,10 @@ int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
  *            its kernel arguments (at most 64 items; same results); 0 = it reads them
  *            from the pinned plan slot.
  *   "dequant_path" 1 = mvllm_hip_dequant decodes through the matrix-core operand path.
- * Shapes the matrix-core kernels do not take (fmt 0, D or Iinter not a multiple of
- * 256, misaligned pointers) run an exact f32 kernel instead. */
+ * fmt 0 experts (f32 weights, the shared experts) run on the f32 matrix cores when
+ * D % 16 == 0, Iinter % 32 == 0, D % 32 == 0 and rows are 16-byte aligned.  Shapes the
+ * matrix-core kernels do not take (D or Iinter not a multiple of 256 for fmt 4/7, odd
+ * fmt 0 shapes, misaligned pointers) run an exact element-wise f32 kernel instead. */
 int mvllm_hip_set_option(const char *key, long long value);
 
 /* ---- segment construction: moe_union_ids (src/model/ops.cpp:1082-1099) and the
@@ -183,6 +185,38 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
                             int *idx, float *wt, int *work, int *eids, int *xoff, int *nr,
                             int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
                             void *stream);
+
+/* ---- the steps either side of the block (device, enqueued on `stream`; 1 = enqueued,
+ *      0 = bad arguments, see mvllm_hip_last_error) --------------------------------- */
+
+/* The router of one MoE layer for n_tok token rows: cpu_route (src/gpu/metal_ops.cpp:
+ * 213-231) of every row -- scores = x . w^T (f32 [n_exp][D] weights, f32 matrix cores),
+ * mix = sigmoid(scores), choice = mix + bias (bias NULL: none), moe_topk(choice, mix),
+ * weights * rscale.  x [n_tok][D], workspaces scores and choice [n_tok][n_exp] f32 (scores
+ * returns the mix), idx / wt [n_tok][k] as mvllm_hip_moe_topk_dev writes them; they feed
+ * mvllm_hip_moe_segments_dev.  The dot products are f32 in another order than the
+ * reference's sequential sum and the sigmoid uses the device's expf, so a score may
+ * differ from the host's by a few ulp: picks agree except where the k-th and (k+1)-th
+ * choices are that close.  D % 16 == 0, n_exp % 32 == 0 (<= 4096), 1 <= k <= min(64,
+ * n_exp), x and w 16-byte aligned. */
+int mvllm_hip_router_dev(const float *x, const float *w, const float *bias, int n_tok, int D,
+                         int n_exp, int k, float rscale, float *scores, float *choice,
+                         int *idx, float *wt, void *stream);
+
+/* A dense linear y[n][O] = x[n][K] . W^T, as QuantMat::gemm (src/quant/weight.cpp:47-64):
+ * K3's latent down / up projections around the routed block (src/model/kimi_k3.cpp:
+ * 2003-2006, 2074-2090).  fmt 0: f32 W [O][K] on the f32 matrix cores (K % 16, O % 32,
+ * 16-byte aligned rows); fmt 4 / 7: W codes [O][K/2] with scales as in moe_block, the
+ * input rows as two bf16 terms (2^-17 relative) on the bf16 matrix cores (K % 256,
+ * O % 256).  QuantMat's int8 rows (fmt 8) are not taken: 0, use the host. */
+int mvllm_hip_linear_dev(int fmt, const void *w, const void *scales, int O, int K,
+                         const float *x, int n, float *y, void *stream);
+
+/* y[r] = rmsnorm(x[r]) with weight w (NULL: none), rows of n: quant::rmsnorm
+ * (src/quant/quant.cpp:384-398), the lat_n norm of K3's routed output
+ * (src/model/kimi_k3.cpp:2074-2079).  The sum of squares is f32 in another order. */
+int mvllm_hip_rmsnorm_dev(const float *x, const float *w, float *y, int rows, int n, float eps,
+                          void *stream);
 
 /* Expert blob geometry (byte offsets of the six pieces inside one expert blob):
  * fmt 4 = GLM gate_p|gate_s|up_p|up_s|down_p|down_s (src/model/glm53.cpp:56-78,

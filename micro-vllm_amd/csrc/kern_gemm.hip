@@ -37,7 +37,9 @@ struct GemmItem {
 
 struct GemmArgs {
     const ExpertWork *ew;
-    const GemmItem *items;
+    const GemmItem *items;  // null: one expert (ew1) over rows [0, nrows_all) in blocks of BM
+    ExpertWork ew1;
+    int nrows_all;
     const __bf16 *pin;  // A planes [TERMS][rcap][K] (int4: 8-blocks in slot order)
     __bf16 *pout;       // dual: H planes [TERMS][rcap][O]
     float *out;         // single: Y [rcap][O] f32
@@ -115,8 +117,15 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         TaskD<FMT> d;
         const int item = task / A.nbn;
         const int nb = task - item * A.nbn;
-        const GemmItem it = A.items[item];
-        const ExpertWork &ew = A.ew[it.a];
+        GemmItem it;
+        if (A.items) {
+            it = A.items[item];
+        } else {
+            it.a = 0;
+            it.r0 = item * BM;
+            it.nrow = min(BM, A.nrows_all - it.r0);
+        }
+        const ExpertWork &ew = A.items ? A.ew[it.a] : A.ew1;
         d.jbase = ew.row0 + it.r0;
         d.nrow = it.nrow;
         d.col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
@@ -537,6 +546,29 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
     if (fmt == 7)
         return dual ? launch_gemm_fd<7, true>(a, n_items, terms, mt, st)
                     : launch_gemm_fd<7, false>(a, n_items, terms, mt, st);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, int nrows,
+                            const void *pin, float *out, int K, int O, hipStream_t st) {
+    if (nrows <= 0)
+        return hipSuccess;
+    if (K % kGemmBK || O % 256 || gemm_lds_bytes(fmt, terms, mt) > 163840 || !ew1)
+        return hipErrorInvalidValue;
+    GemmArgs a{};
+    a.ew1 = *ew1;
+    a.nrows_all = nrows;
+    a.pin = static_cast<const __bf16 *>(pin);
+    a.out = out;
+    a.nbn = O / 256;
+    a.K = K;
+    a.O = O;
+    a.rcap = nrows;
+    const int n_items = (nrows + 16 * mt - 1) / (16 * mt);
+    if (fmt == 4)
+        return launch_gemm_fd<4, false>(a, n_items, terms, mt, st);
+    if (fmt == 7)
+        return launch_gemm_fd<7, false>(a, n_items, terms, mt, st);
     return hipErrorInvalidValue;
 }
 

@@ -159,8 +159,31 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act, float act_a, float act_b,
                        hipStream_t st);
+// One matrix (w[2], s[2] of *ew1) over input rows [0, nrows) of the planes, in items of
+// 16 * mt rows computed in the kernel (a dense linear): out [nrows][O] f32.
+hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, int nrows,
+                            const void *pin, float *out, int K, int O, hipStream_t st);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
                               int K, int rcap, void *planes, hipStream_t st);
+
+// f32-weight GEMMs on the matrix cores (kern_f32.hip): fmt 0 moe_block, router scores,
+// fmt 0 linears.  Items {expert, r0, nrow, 0} of <= 16 * mt rows (mt 1, 2, 4), or, with
+// items null, one expert *ew1 over rows [0, nrows_all) in blocks of 16 * mt.  dual: gate
+// w[0] and up w[1] -> act -> out [rcap][O]; single: w[mi] -> out.  Input row of compact
+// row j: in_rows[j] (or j).  Requires K % 16 == 0, O % 16 (dual) / % 32 (single) == 0,
+// 16-byte aligned weight and input rows.
+bool f32mm_fits(bool dual, int K, int O);
+hipError_t launch_f32mm(bool dual, int mt, const ExpertWork *ew, const void *items, int n_items,
+                        const ExpertWork *ew1, int nrows_all, const float *in,
+                        const int *in_rows, float *out, int mi, int K, int O, int act,
+                        float act_a, float act_b, hipStream_t st);
+// Router tail: scores -> sigmoid in place (the mix), choice = mix + bias; then w *= rscale.
+hipError_t launch_route_tail(float *scores, const float *bias, float *choice, int n, int E,
+                             hipStream_t st);
+hipError_t launch_scale(float *w, size_t count, float rscale, hipStream_t st);
+// y[r] = rmsnorm(x[r]) * w (w may be null), rows of n.
+hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int rows, int n, float eps,
+                          hipStream_t st);
 
 // Native MXFP4 GEMM (kern_fp4.hip): v_mfma_scale_f32_16x16x128_f8f6f4 with e2m1 activations
 // (codes [rcap][K/2] + ue8m0 scales [rcap][K/32], from launch_quantize_mxfp4) against the

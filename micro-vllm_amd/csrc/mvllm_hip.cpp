@@ -159,6 +159,7 @@ struct Ctx {
     void *scratch_ptr = nullptr;     // device address of `scratch` on `device`
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
+    DevBuf Lp;  // planes of mvllm_hip_linear_dev's input rows
     HostBuf hx, ho;
     // Plan slots, reused in groups of kGroup: one event after a group's last call guards
     // the reuse of all its slots.  A group whose last call did not reach finish_call is
@@ -359,6 +360,7 @@ struct CallCfg {
     bool mfma = false;        // decode-shaped matrix-core kernels
     bool gemm = false;        // grouped GEMM (prefill-shaped)
     bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
+    bool f32 = false;         // fmt 0: the f32 matrix-core GEMM (kern_f32.hip)
     bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
@@ -451,7 +453,7 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
 // smallest class that holds it; classes ordered by mt, experts ascending within each.
 void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     cc.terms = cc.terms >= 2 ? 2 : 1;
-    const int max_mt = cc.fp4 ? kFp4MaxMt : gemm_max_mt(fmt, cc.terms);
+    const int max_mt = cc.f32 ? 4 : cc.fp4 ? kFp4MaxMt : gemm_max_mt(fmt, cc.terms);
     const int bm = 16 * max_mt;
     std::vector<int> per[4];  // class index = log2(mt)
     size_t split_at[4] = {0, 0, 0, 0};
@@ -482,7 +484,7 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
         cc.items.insert(cc.items.end(), per[c].begin(), per[c].end());
         g.it1 = cc.items.size() / 4;
     }
-    cc.gemm = true;
+    cc.gemm = !cc.f32;
 }
 
 // ordered: the combine keeps the reference's expert order even for decode-shaped calls
@@ -497,6 +499,18 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
     bool ok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && D <= kDecMaxK &&
               I <= kDecMaxK && aligned(in, 16);
     bool gok = (fmt == 4 || fmt == 7) && D % 256 == 0 && I % 256 == 0 && aligned(in, 16);
+    // fmt 0 (f32 weights, the shared experts): the f32 matrix-core GEMM for every row count
+    if (fmt == 0 && f32mm_fits(true, D, I) && f32mm_fits(false, I, D) && aligned(in, 16)) {
+        bool al = true;
+        for (const ExpertWork &w : P.ew)
+            for (int m = 0; m < 3; ++m)
+                al = al && aligned(w.w[m], 16);
+        if (al) {
+            cc.f32 = true;
+            plan_gemm(cc, P, split, fmt);
+            return;
+        }
+    }
     const size_t walign = fmt == 7 && C.fp4act ? 16 : 8;  // the FP4 GEMM loads 16-byte rows
     int most = 0;
     for (const ExpertWork &w : P.ew) {
@@ -548,7 +562,10 @@ void buf_sizes(const CallCfg &cc, size_t R, int D, int I, size_t sz[5]) {
     const size_t tb = (size_t)cc.terms * 2;
     for (int i = 0; i < 5; ++i)
         sz[i] = 0;
-    if (cc.fp4) {
+    if (cc.f32) {
+        sz[0] = R * I * 4;
+        sz[1] = R * D * 4;
+    } else if (cc.fp4) {
         sz[0] = R * I * 4;
         sz[1] = R * D * 4;
         sz[2] = R * (I / 2 + I / 32);
@@ -861,6 +878,34 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
                                     static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f, st));
             C.stats[14] += 1;
         }
+    } else if (cc.f32) {
+        // f32 matrix cores on the f32 rows themselves (no planes): gate/up + act -> H f32,
+        // down -> Y
+        HIP_TRY(mark(1));
+        for (int part = 0; part < 2; ++part) {
+            if (part == 1 && gate_event)
+                HIP_TRY(hipStreamWaitEvent(st, gate_event, 0));
+            for (int c = 0; c < cc.n_gcls; ++c) {
+                const GemmCls &g = cc.gcls[c];
+                const size_t i0 = part ? g.it_split : g.it0, i1 = part ? g.it1 : g.it_split;
+                if (i1 <= i0)
+                    continue;
+                HIP_TRY(launch_f32mm(true, g.mt, dp.ew, dp.items + 4 * i0,
+                                     static_cast<int>(i1 - i0), nullptr, 0, in, in_rows,
+                                     static_cast<float *>(B.H), 0, D, I, act, a, b, st));
+                C.stats[13] += 1;
+            }
+        }
+        HIP_TRY(mark(2));
+        HIP_TRY(mark(3));
+        for (int c = 0; c < cc.n_gcls; ++c) {
+            const GemmCls &g = cc.gcls[c];
+            HIP_TRY(launch_f32mm(false, g.mt, dp.ew, dp.items + 4 * g.it0,
+                                 static_cast<int>(g.it1 - g.it0), nullptr, 0,
+                                 static_cast<const float *>(B.H), nullptr,
+                                 static_cast<float *>(B.Y), 2, I, D, 0, 0.f, 0.f, st));
+            C.stats[14] += 1;
+        }
     } else if (cc.gemm) {
         HIP_TRY(launch_prep_planes(fmt, cc.terms, in, in_rows, rcap, D, rcap, B.Xp, st));
         HIP_TRY(mark(1));
@@ -1150,6 +1195,7 @@ void mvllm_hip_shutdown(void) {
     C.Ph.release();
     C.HP.release();
     C.Xp.release();
+    C.Lp.release();
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
@@ -1666,6 +1712,77 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
     }
     HIP_TRY(launch_moe_route(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, rows, rw,
                              cap_experts, cap_rows, counts, static_cast<hipStream_t>(stream)));
+    return 1;
+}
+
+int mvllm_hip_router_dev(const float *x, const float *w, const float *bias, int n_tok, int D,
+                         int n_exp, int k, float rscale, float *scores, float *choice,
+                         int *idx, float *wt, void *stream) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !x || !w || !scores || !choice || !idx || !wt || n_tok < 1 || D < 1 ||
+        n_exp < 1 || n_exp > kRouteMaxExperts || k < 1 || k > 64 || k > n_exp ||
+        !f32mm_fits(false, D, n_exp) || !aligned(x, 16) || !aligned(w, 16)) {
+        set_err("router_dev: bad arguments (D % 16, n_exp % 32, 16-byte aligned rows, "
+                "1 <= k <= min(64, n_exp), n_exp <= 4096)");
+        return 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ExpertWork ew{};
+    ew.w[0] = w;
+    const int mt = n_tok <= 16 ? 1 : n_tok <= 32 ? 2 : 4;
+    HIP_TRY(launch_f32mm(false, mt, nullptr, nullptr, 0, &ew, n_tok, x, nullptr, scores, 0, D,
+                         n_exp, 0, 0.f, 0.f, st));
+    HIP_TRY(launch_route_tail(scores, bias, choice, n_tok, n_exp, st));
+    HIP_TRY(launch_moe_topk(choice, scores, n_tok, n_exp, k, idx, wt, st));
+    if (rscale != 1.f)
+        HIP_TRY(launch_scale(wt, (size_t)n_tok * k, rscale, st));
+    return 1;
+}
+
+int mvllm_hip_linear_dev(int fmt, const void *w, const void *scales, int O, int K,
+                         const float *x, int n, float *y, void *stream) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    const bool q = fmt == 4 || fmt == 7;
+    if (!C.ready || !w || !x || !y || n < 1 || (fmt != 0 && !q) || (q && !scales) ||
+        (fmt == 0 && (!f32mm_fits(false, K, O) || !aligned(w, 16) || !aligned(x, 16))) ||
+        (q && (K % 256 || O % 256 || !aligned(w, 8) || !aligned(scales, fmt == 4 ? 16 : 8)))) {
+        set_err("linear_dev: bad arguments (fmt 0: K % 16, O % 32, 16-byte aligned rows; "
+                "fmt 4/7: K % 256, O % 256, 8-byte aligned codes, aligned scales)");
+        return 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    ExpertWork ew{};
+    if (fmt == 0) {
+        ew.w[0] = w;
+        const int mt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
+        HIP_TRY(launch_f32mm(false, mt, nullptr, nullptr, 0, &ew, n, x, nullptr, y, 0, K, O, 0,
+                             0.f, 0.f, st));
+        return 1;
+    }
+    // quantized: the input rows as two bf16 terms (2^-17 relative), then the grouped GEMM
+    ew.w[2] = w;
+    ew.s[2] = scales;
+    const int terms = 2;
+    HIP_TRY(C.Lp.ensure((size_t)terms * 2 * n * K));
+    HIP_TRY(launch_prep_planes(fmt, terms, x, nullptr, n, K, n, C.Lp.p, st));
+    const int mt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
+    HIP_TRY(launch_gemm_rows(fmt, terms, mt, &ew, n, C.Lp.p, y, K, O, st));
+    return 1;
+}
+
+int mvllm_hip_rmsnorm_dev(const float *x, const float *w, float *y, int rows, int n, float eps,
+                          void *stream) {
+    Ctx &C = ctx();
+    set_err("");
+    if (!C.ready || !x || !y || rows < 1 || n < 1) {
+        set_err("rmsnorm_dev: bad arguments");
+        return 0;
+    }
+    HIP_TRY(launch_rmsnorm(x, w, y, rows, n, eps, static_cast<hipStream_t>(stream)));
     return 1;
 }
 

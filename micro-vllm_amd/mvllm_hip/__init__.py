@@ -59,6 +59,9 @@ _SIGS = {
     "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
     "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
     "mvllm_hip_bf16_planes": (_i, [_i, _i, _p, _i, _i, _p]),
+    "mvllm_hip_router_dev": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _p, _p, _p, _p, _p]),
+    "mvllm_hip_linear_dev": (_i, [_i, _p, _p, _i, _i, _p, _i, _p, _p]),
+    "mvllm_hip_rmsnorm_dev": (_i, [_p, _p, _p, _i, _i, _f, _p]),
     "mvllm_hip_moe_topk_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p]),
     "mvllm_hip_moe_segments_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _i, _i, _p,
                                         _p]),
@@ -259,6 +262,24 @@ def moe_route_dev(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, r
                                          _ptr(wt), _ptr(work), _ptr(eids), _ptr(xoff), _ptr(nr),
                                          _ptr(rows), _ptr(rw), len(eids), len(rows), _ptr(counts),
                                          _stream(stream)), "mvllm_hip_moe_route_dev")
+
+
+def router_dev(x, w, bias, n_tok, D, n_exp, k, rscale, scores, choice, idx, wt, stream=None):
+    """cpu_route of every token row on the device (see mvllm_hip_router_dev); enqueued."""
+    _check(lib().mvllm_hip_router_dev(_ptr(x), _ptr(w), _ptr(bias), n_tok, D, n_exp, k, rscale,
+                                      _ptr(scores), _ptr(choice), _ptr(idx), _ptr(wt),
+                                      _stream(stream)), "mvllm_hip_router_dev")
+
+
+def linear_dev(fmt, w, scales, O, K, x, n, y, stream=None):
+    """y[n, O] = x[n, K] . W^T on the device (see mvllm_hip_linear_dev); enqueued."""
+    _check(lib().mvllm_hip_linear_dev(fmt, _ptr(w), _ptr(scales), O, K, _ptr(x), n, _ptr(y),
+                                      _stream(stream)), "mvllm_hip_linear_dev")
+
+
+def rmsnorm_dev(x, w, y, rows, n, eps, stream=None):
+    _check(lib().mvllm_hip_rmsnorm_dev(_ptr(x), _ptr(w), _ptr(y), rows, n, eps,
+                                       _stream(stream)), "mvllm_hip_rmsnorm_dev")
 
 
 def bf16_planes(fmt, terms, x_dev, n, K, planes_dev):

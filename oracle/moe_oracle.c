@@ -497,3 +497,52 @@ int orc_moe_block_fp4act(int nb, int D, int Iinter, int fmt, int qgs, const void
     }
     return 1;
 }
+
+/* ---- the steps either side of the block --------------------------------------- */
+
+/* quant::rmsnorm (src/quant/quant.cpp:384-398): sequential f32 sum of squares, one
+ * reciprocal square root, then x * inv * w in that order. */
+void orc_rmsnorm(const float *x, const float *w, float *y, int n, float eps) {
+    if (n <= 0)
+        return;
+    float ss = 0.f;
+    for (int i = 0; i < n; ++i)
+        ss += x[i] * x[i];
+    const float inv = 1.f / sqrtf(ss / (float)n + eps);
+    if (w) {
+        for (int i = 0; i < n; ++i)
+            y[i] = x[i] * inv * w[i];
+    } else {
+        for (int i = 0; i < n; ++i)
+            y[i] = x[i] * inv;
+    }
+}
+
+/* cpu_route (src/gpu/metal_ops.cpp:213-231) for one row: scores = matmul_f32(x, w),
+ * mix = sigmoid(scores), choice = mix + bias (0 without), moe_topk(choice, mix), then the
+ * first min(k, E) weights times rscale when rscale != 1. */
+void orc_route(const float *x, const float *w, const float *bias, int D, int E, int k,
+               float rscale, int *idx, float *wt) {
+    if (!x || !w || !idx || !wt || D < 1 || E < 1 || k < 1)
+        return;
+    float *scores = (float *)calloc((size_t)E, sizeof(float));
+    float *choice = (float *)calloc((size_t)E, sizeof(float));
+    if (!scores || !choice) {
+        free(scores);
+        free(choice);
+        return;
+    }
+    orc_matmul_f32(scores, x, w, 1, D, E);
+    for (int i = 0; i < E; ++i) {
+        scores[i] = orc_sigmoid(scores[i]);
+        choice[i] = scores[i] + (bias ? bias[i] : 0.f);
+    }
+    orc_moe_topk(choice, E, k, idx, wt, scores);
+    if (rscale != 1.f) {
+        const int kk = k > E ? E : k;
+        for (int i = 0; i < kk; ++i)
+            wt[i] *= rscale;
+    }
+    free(scores);
+    free(choice);
+}

@@ -93,6 +93,12 @@ float orc_e2m1_decode(uint8_t nib);
 int orc_fp4_activation_qdq(float *output, uint8_t *scales, const float *input, int length,
                            int block_size, uint8_t *codes);
 
+/* The steps either side of the block: quant::rmsnorm (src/quant/quant.cpp:384-398) and
+ * cpu_route (src/gpu/metal_ops.cpp:213-231) of one row. */
+void orc_rmsnorm(const float *x, const float *w, float *y, int n, float eps);
+void orc_route(const float *x, const float *w, const float *bias, int D, int E, int k,
+               float rscale, int *idx, float *wt);
+
 #ifdef __cplusplus
 }
 #endif

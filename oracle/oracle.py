@@ -82,6 +82,8 @@ class CpuMoe:
                 "dequant_mxfp4": (None, [_p, _p, _p, _i, _i]),
                 "moe_segments": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
                 "fp4_activation_qdq": (_i, [_p, _p, _p, _i, _i, _p]),
+                "rmsnorm": (None, [_p, _p, _p, _i, _f]),
+                "route": (None, [_p, _p, _p, _i, _i, _i, _f, _p, _p]),
                 "moe_block_fp4act": (_i, [_i, _i, _i, _i, _i, _pp, _pp, _pp, _pp, _pp, _pp, _p,
                                           _p, _p, _p, _p, _p, _i, _i, _f, _f]),
             }.items():
@@ -93,7 +95,10 @@ class CpuMoe:
             for name, args in {"quantize_int4_g64": [_p, _i, _i, _p, _p],
                                "pack_mxfp4": [_p, _i, _i, _p, _p],
                                "silu_mul": [_p, _p, _i],
-                               "bf16_round_array": [_p, _i]}.items():
+                               "bf16_round_array": [_p, _i],
+                               "rmsnorm": [_p, _p, _p, _i, _f],
+                               "norm_route": [_p, _p, _i, _f, _p, _p, _i, _i, _f, _p, _p,
+                                              _p]}.items():
                 fn = getattr(L, f"ref_{name}")
                 fn.restype, fn.argtypes = None, args
 
@@ -112,6 +117,48 @@ class CpuMoe:
 
     def bf16_round(self, v):
         return self.fn("bf16_round")(v)
+
+    def rmsnorm(self, x, w, eps):
+        """quant::rmsnorm of each row of x (w may be None)."""
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty_like(x)
+        n = x.shape[-1]
+        wp = None if w is None else np.ascontiguousarray(w, np.float32)
+        for r in range(x.size // n):
+            self.fn("rmsnorm")(x.ctypes.data + 4 * n * r, None if wp is None else wp.ctypes.data,
+                               y.ctypes.data + 4 * n * r, n, eps)
+        return y
+
+    def route(self, x, w, bias, k, rscale=1.0):
+        """cpu_route of each row of x (oracle only): -> idx [rows, k], wt [rows, k]."""
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w, np.float32)
+        E, D = w.shape
+        rows = x.size // D
+        idx = np.zeros((rows, k), np.int32)
+        wt = np.zeros((rows, k), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        for r in range(rows):
+            self.fn("route")(x.ctypes.data + 4 * D * r, w.ctypes.data,
+                             None if b is None else b.ctypes.data, D, E, k, rscale,
+                             idx.ctypes.data + 4 * k * r, wt.ctypes.data + 4 * k * r)
+        return idx, wt
+
+    def norm_route(self, x, post_ln, eps, w, bias, k, rscale=1.0):
+        """_ref only: metal_ops::layer_decode_full's host path on one row x:
+        -> (nrm = rmsnorm(x, post_ln), idx, wt = cpu_route(nrm))."""
+        x = np.array(x, np.float32, copy=True)
+        w = np.ascontiguousarray(w, np.float32)
+        E, D = w.shape
+        nrm = np.zeros(D, np.float32)
+        idx = np.zeros(k, np.int32)
+        wt = np.zeros(k, np.float32)
+        p = None if post_ln is None else np.ascontiguousarray(post_ln, np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        self.lib.ref_norm_route(x.ctypes.data, None if p is None else p.ctypes.data, D, eps,
+                                w.ctypes.data, None if b is None else b.ctypes.data, E, k,
+                                rscale, nrm.ctypes.data, idx.ctypes.data, wt.ctypes.data)
+        return nrm, idx, wt
 
     def bf16_round_array(self, x):
         """The reference's bf16_round_array (src/quant/bf16.cpp:36-41) on a copy of x

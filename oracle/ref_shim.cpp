@@ -59,6 +59,19 @@ int ref_moe_union_ids(const int *idx, int n_tok, int topk, int *out, int cap) {
 }
 
 float ref_bf16_round(float v) { return bf16_round(v); }
+void ref_rmsnorm(const float *x, const float *w, float *y, int n, float eps) {
+    quant::rmsnorm(x, w, y, n, eps);
+}
+// The reference's own router (cpu_route, file-local in metal_ops.cpp) through its public
+// host path: metal_ops::layer_decode_full with no attention, no shared expert and the
+// library never initialised runs rmsnorm(x, post_ln) -> nrm, then cpu_route(nrm).
+void ref_norm_route(float *x, const float *post_ln, int D, float eps, const float *w,
+                    const float *bias, int E, int K, float rscale, float *nrm, int *idx,
+                    float *wt) {
+    metal_ops::layer_decode_full(x, nullptr, nullptr, post_ln, nullptr, nullptr, nullptr, D, 0,
+                                 eps, metal_ops::Act::Silu, 0.f, 0.f, w, bias, E, K, rscale,
+                                 nullptr, nrm, nullptr, idx, wt);
+}
 void ref_bf16_round_array(float *v, int n) { bf16_round_array(v, n); }
 float ref_e8m0_decode(uint8_t v) { return e8m0_decode(v); }
 float ref_e2m1_decode(uint8_t v) { return e2m1_decode(v); }

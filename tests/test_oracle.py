@@ -428,3 +428,66 @@ def test_fp4act_close_to_f32(orc):
     assert 1e-4 < err < 0.3
     c4 = random_case(rng, 4, 64, 64, [1], 1)
     assert orc.moe_block_fp4act(*c4.args(), 0, 0.0, 0.0) == 0
+
+
+# ---- the steps either side of the block: rmsnorm and the router ------------------------
+
+def test_rmsnorm_bit_exact_vs_ref(orc, ref):
+    """orc_rmsnorm equals quant::rmsnorm (src/quant/quant.cpp:384-398) bit for bit."""
+    rng = np.random.default_rng(5)
+    for n, eps, with_w in ((1, 1e-6, True), (7, 1e-5, False), (2048, 1e-6, True),
+                           (7168, 1e-6, True), (333, 0.0, False)):
+        x = (rng.standard_normal((3, n)) * rng.uniform(0.1, 50)).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32) if with_w else None
+        a, b = orc.rmsnorm(x, w, eps), ref.rmsnorm(x, w, eps)
+        assert np.array_equal(_bits(a), _bits(b)), (n, eps, with_w)
+
+
+def test_rmsnorm_closed_form(orc):
+    """A row of equal values c normalises to sign(c) / sqrt(1 + eps / c^2) times w."""
+    x = np.full((1, 64), -3.0, np.float32)
+    w = np.full(64, 2.0, np.float32)
+    y = orc.rmsnorm(x, w, 0.0)
+    assert np.allclose(y, -2.0, rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("D,E,k,rscale,ties", [(256, 64, 8, 1.0, False), (512, 384, 8, 2.5, False),
+                                               (128, 32, 4, 1.0, True), (1024, 96, 6, 0.5, True)])
+def test_norm_route_bit_exact_vs_ref(orc, ref, D, E, k, rscale, ties):
+    """The oracle's rmsnorm -> cpu_route composition equals the reference's own router
+    (file-local cpu_route, src/gpu/metal_ops.cpp:213-231, reached through its public host
+    path metal_ops::layer_decode_full, :233-254): normalised row, picks and weights, bit for
+    bit, with and without a bias, including equal router rows (ties: lower index first)."""
+    rng = np.random.default_rng(D + E + k)
+    w = (rng.standard_normal((E, D)) * 0.05).astype(np.float32)
+    if ties:
+        w[5] = w[2]
+        w[E - 1] = w[0]
+    post_ln = rng.uniform(0.5, 1.5, D).astype(np.float32)
+    for rep in range(4):
+        x = rng.standard_normal(D).astype(np.float32)
+        bias = (rng.standard_normal(E) * 0.01).astype(np.float32) if rep % 2 else None
+        nrm_r, idx_r, wt_r = ref.norm_route(x, post_ln, 1e-6, w, bias, k, rscale)
+        nrm_o = orc.rmsnorm(x[None, :], post_ln, 1e-6)[0]
+        idx_o, wt_o = orc.route(nrm_o, w, bias, k, rscale)
+        assert np.array_equal(_bits(nrm_o), _bits(nrm_r))
+        assert np.array_equal(idx_o[0], idx_r)
+        assert np.array_equal(_bits(wt_o[0]), _bits(wt_r))
+
+
+def test_route_closed_form(orc):
+    """Identity router rows make each score exactly x[e]: the picks are the k largest
+    sigmoid(x) + bias (ties to the lower index) and the weights their sigmoids over the
+    sum, times rscale."""
+    rng = np.random.default_rng(77)
+    E = 48
+    x = rng.permutation(np.linspace(-4, 4, E)).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.3).astype(np.float32)
+    w = np.eye(E, dtype=np.float32)
+    idx, wt = orc.route(x, w, bias, 6, 1.5)
+    sig = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    choice = sig + bias
+    exp_idx = np.argsort(-choice, kind="stable")[:6]
+    assert np.array_equal(idx[0], exp_idx)
+    exp_w = sig[exp_idx] / sig[exp_idx].sum() * 1.5
+    assert np.allclose(wt[0], exp_w, rtol=2e-6, atol=0)
