@@ -37,7 +37,7 @@ struct GemmItem {
 
 struct GemmArgs {
     const ExpertWork *ew;
-    const GemmItem *items;  // null: one expert (ew1) over rows [0, nrows_all) in blocks of BM
+    const GemmItem *items;  // per item (UNI kernels: none; one expert ew1 over nrows_all rows)
     ExpertWork ew1;
     int nrows_all;
     const __bf16 *pin;  // A planes [TERMS][rcap][K] (int4: 8-blocks in slot order)
@@ -90,10 +90,12 @@ struct TaskD {
     int jbase, nrow, col0;
 };
 
-// One workgroup per task.  The 32-row class with one term is held to 128 VGPRs (4 waves per SIMD), so two
+// One workgroup per task.  UNI: one expert (A.ew1) over rows [0, A.nrows_all) in blocks of
+// BM, no item list (dense linears; a template parameter so that the selection costs the
+// grouped form no registers).  The 32-row class with one term is held to 128 VGPRs (4 waves per SIMD), so two
 // workgroups share a CU: it needs 126-131 VGPRs, and the cap costs at most a few spilled
 // registers.  Measured on c3: 1.60 -> 1.53 ms per call.
-template <int FMT, bool DUAL, int TERMS, int MT>
+template <int FMT, bool DUAL, int TERMS, int MT, bool UNI>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
     constexpr int BM = 16 * MT;
@@ -118,14 +120,14 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         const int item = task / A.nbn;
         const int nb = task - item * A.nbn;
         GemmItem it;
-        if (A.items) {
-            it = A.items[item];
-        } else {
+        if constexpr (UNI) {
             it.a = 0;
             it.r0 = item * BM;
             it.nrow = min(BM, A.nrows_all - it.r0);
+        } else {
+            it = A.items[item];
         }
-        const ExpertWork &ew = A.items ? A.ew[it.a] : A.ew1;
+        const ExpertWork &ew = UNI ? A.ew1 : A.ew[it.a];
         d.jbase = ew.row0 + it.r0;
         d.nrow = it.nrow;
         d.col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
@@ -473,10 +475,10 @@ static bool g_gemm_xcd = true;  // option "gemm_xcd"
 void gemm_set_xcd(bool on) { g_gemm_xcd = on; }
 bool gemm_xcd() { return g_gemm_xcd; }
 
-template <int FMT, bool DUAL, int TERMS, int MT>
+template <int FMT, bool DUAL, int TERMS, int MT, bool UNI = false>
 static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
     const size_t lds = gemm_lds_bytes(FMT, TERMS, MT);
-    auto kern = k_gemm<FMT, DUAL, TERMS, MT>;
+    auto kern = k_gemm<FMT, DUAL, TERMS, MT, UNI>;
     static bool attr = false;  // the dynamic LDS limit, raised once per process
     if (!attr) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(kern),
@@ -565,10 +567,18 @@ hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, i
     a.O = O;
     a.rcap = nrows;
     const int n_items = (nrows + 16 * mt - 1) / (16 * mt);
+    if (terms != 2)
+        return hipErrorInvalidValue;
+#define MVLLM_ROWS(F)                                                                          \
+    return mt == 1 ? launch_gemm_t<F, false, 2, 1, true>(a, n_items, st)                      \
+         : mt == 2 ? launch_gemm_t<F, false, 2, 2, true>(a, n_items, st)                      \
+         : mt == 4 ? launch_gemm_t<F, false, 2, 4, true>(a, n_items, st)                      \
+                   : hipErrorInvalidValue
     if (fmt == 4)
-        return launch_gemm_fd<4, false>(a, n_items, terms, mt, st);
+        MVLLM_ROWS(4);
     if (fmt == 7)
-        return launch_gemm_fd<7, false>(a, n_items, terms, mt, st);
+        MVLLM_ROWS(7);
+#undef MVLLM_ROWS
     return hipErrorInvalidValue;
 }
 
