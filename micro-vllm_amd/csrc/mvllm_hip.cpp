@@ -714,9 +714,18 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
             C.slot_next = si;
             return 0;
         }
-    } else {
-        HIP_TRY(s.host.ensure(total));
-        HIP_TRY(s.dev.ensure(total));
+    } else if (total > s.host.cap || total > s.dev.cap) {
+        // Every slot grows together, once per new plan size: freeing pinned memory drains
+        // the device, and slots growing one by one on their first use at a size would
+        // drain it once per slot, in the middle of a stream of calls.
+        HIP_TRY(hipDeviceSynchronize());
+        for (auto &g : C.grp_used)
+            g = false;  // every earlier call is done
+        const size_t want = std::max(total, std::max(s.host.cap, s.dev.cap) * 3 / 2);
+        for (PlanSlot &t : C.slots) {
+            HIP_TRY(t.host.ensure(want));
+            HIP_TRY(t.dev.ensure(want));
+        }
     }
     char *dbase = dev_dst ? static_cast<char *>(dev_dst) : static_cast<char *>(s.dev.p);
     char *h = static_cast<char *>(s.host.p);
