@@ -186,6 +186,30 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
                             int *rows, float *rw, int cap_experts, int cap_rows, int *counts,
                             void *stream);
 
+/* moe_block on segments that are already in device memory, with no host round trip:
+ * the per-expert loop of the engines' batched MoE (src/model/glm53.cpp:1938-1992) fed by
+ * mvllm_hip_moe_route_dev / mvllm_hip_moe_segments_dev, whose outputs it reads as they
+ * are: counts[0] = segments, counts[1] = compact rows; segment i is expert eids[i] with
+ * compact rows [xoff[i], xoff[i] + nr[i]); compact row j is token rows[j] of x with
+ * weight rw[j].  Expert e's weights are the blob at table[e] (device array of n_table
+ * blob addresses in the reference blob layout, 256-byte aligned: a slab's table, or the
+ * HBM tier's blobs); an id outside [0, n_table), a null entry or a misaligned one
+ * consumes its rows without writing (the reference's null-expert rule,
+ * src/gpu/metal_ops.cpp:291-296).  x [S][D] token rows, out [S][D] accumulated with
+ * += in expert order (src/gpu/metal_ops.cpp:328-339).  The plan (expert work, grouped-
+ * GEMM items, the combine lists) is built by kernels; launches are sized for the caps
+ * (cap_experts segments, cap_rows compact rows) and their surplus workgroups exit.
+ * Arithmetic: the grouped GEMM with two bf16 terms per activation (2^-17) when cap_rows
+ * <= 256, one above (mode option 1: always two, 2: always one).  fmt 4 / 7, D and Iinter
+ * multiples of 256, 1 <= S <= 65535.  status (device int, may be NULL) receives 0, or 2
+ * when a blob address was not 256-byte aligned.  Enqueued on `stream`; 1 enqueued. */
+int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const *table,
+                                   int n_table, const int *counts, const int *eids,
+                                   const int *xoff, const int *nr, int cap_experts,
+                                   const int *rows, const float *rw, int cap_rows,
+                                   const float *x, float *out, int S, int act, float act_a,
+                                   float act_b, int *status, void *stream);
+
 /* ---- the steps either side of the block (device, enqueued on `stream`; 1 = enqueued,
  *      0 = bad arguments, see mvllm_hip_last_error) --------------------------------- */
 
@@ -224,6 +248,44 @@ int mvllm_hip_rmsnorm_dev(const float *x, const float *w, float *y, int rows, in
  * (src/model/kimi_k3.cpp:83-102, 132-159).  off[6] = gate_p, gate_s, up_p, up_s,
  * down_p, down_s.  Returns the blob size in bytes, or -1 for a bad fmt/shape. */
 long long mvllm_expert_geom(int fmt, int D, int Iinter, long long off[6]);
+
+/* ---- expert containers -> device slabs --------------------------------------- */
+
+/* Where each routed expert's six pieces lie in the safetensors containers of `dir`
+ * (host only, no device).  Replaces the expert registration of the engines' loaders:
+ * src/model/glm53.cpp:1829-1871 (fmt 4: "<prefix>layers.<L>.mlp.experts.<e>.
+ * {gate,up,down}_proj.weight" U8/I8 codes + ".qs" f32 scales) and
+ * src/model/kimi_k3.cpp:1881-1934 (fmt 7: "<prefix>model.layers.<L>.block_sparse_moe.
+ * experts.<e>.w{1,2,3}.weight_{packed,scale}"), over the container reader of
+ * src/io/safetensors.cpp (st_open_dir: every "*.safetensors" file in name order, a name
+ * resolving to the first file that holds it).  Each piece's byte count must equal the blob
+ * geometry's (mvllm_expert_geom for D, Iinter), as the reference requires.  For layers
+ * [layer0, layer1) and experts [0, n_experts), piece k of blob b = (L - layer0) *
+ * n_experts + e (k in blob order: GLM gate_p gate_s up_p up_s down_p down_s, K3 w1p w1s
+ * w2p w2s w3p w3s) is file[6b+k] (index into the sorted file list, written to `paths`
+ * one path a line when paths is not NULL), absolute byte offset[6b+k], bytes[6b+k].
+ * Returns the number of files, or -1 with the reference's message in err
+ * ("glm53 expert pieces missing or wrong size at L<L> E<e>", ...). */
+int mvllm_st_expert_pieces(const char *dir, const char *prefix, int fmt, int D, int Iinter,
+                           int layer0, int layer1, int n_experts, int *file, long long *offset,
+                           long long *bytes, char *paths, long long paths_cap, char *err,
+                           long long err_cap);
+
+/* Reads those pieces into one device allocation: blob b at base + b * stride (stride =
+ * the blob size rounded up to 256 bytes), its six pieces back to back in the blob
+ * layout (so the blob address plus mvllm_expert_geom's offsets give the six pointers of
+ * moe_block), and a device table of the blob addresses (const void *[n_blobs], indexed
+ * (L - layer0) * n_experts + e).  The ExpertStore reads the same pieces into pinned host
+ * slots on demand (src/store/expert_store.cpp); this places a layer range in HBM at
+ * once.  File reads overlap the host-to-device copies (two pinned staging buffers);
+ * synchronous.  Returns a handle > 0, or 0 (see mvllm_hip_last_error). */
+long long mvllm_hip_slab_load(const char *dir, const char *prefix, int fmt, int D, int Iinter,
+                              int layer0, int layer1, int n_experts);
+/* The slab's device base, device table, blob stride and size, and blob count.  1 ok. */
+int mvllm_hip_slab_info(long long slab, void **base, void **table, long long *stride,
+                        long long *blob_bytes, int *n_blobs);
+/* Waits for the device, frees the slab.  1 ok, 0 unknown handle. */
+int mvllm_hip_slab_free(long long slab);
 
 /* ---- HBM expert residency (the LRU tier in front of ExpertStore,
  *      src/store/expert_store.hpp:71-175).  Blobs are keyed by (layer, eid). -- */

@@ -1,0 +1,233 @@
+// kern_dplan.hip -- the plan of a moe_block call whose segments live in device memory
+// (as mvllm_hip_moe_segments_dev writes them), built on the device: no host round trip
+// between routing and the block.
+//
+// The host-planned call (build_plan / plan_gemm in mvllm_hip.cpp) turns the segments
+// into per-expert work, grouped-GEMM items in row classes, and the combine's per-token
+// lists.  Here the same three come from kernels:
+//   k_dplan   one workgroup: per segment i, expert work from the blob table (blob address
+//             of expert eids[i] + the blob geometry's piece offsets), its rows'
+//             liveness, and its grouped-GEMM items (full blocks of BM rows in the top
+//             class, the remainder in the smallest class that holds it), written per
+//             class in expert order by a workgroup scan, with the class item counts;
+//   k_csr_*   the combine lists: per out row t, the compact rows j with rows[j] == t of
+//             experts that are present, in ascending j (= the reference's expert order,
+//             src/gpu/metal_ops.cpp:328-339): count, scan, place, then a per-row sort.
+// A segment whose expert id is outside the table, or whose table entry is null, consumes
+// its rows without writing (the reference's null-expert rule, metal_ops.cpp:291-296).
+#include "mfma_common.h"
+
+#include <algorithm>
+
+namespace mvllm_hip {
+
+constexpr int kPlanThreads = 1024;
+
+__device__ __forceinline__ int dplan_class(int n) {
+    return n <= 16 ? 0 : n <= 32 ? 1 : n <= 64 ? 2 : 3;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
+    __shared__ int part[kPlanThreads][4];
+    __shared__ int tot[4];
+    const int tid = threadIdx.x;
+    const int nb = min(max(A.counts[0], 0), A.cap_e);
+    const int nrows = min(max(A.counts[1], 0), A.cap_rows);
+    for (int j = tid; j < nrows; j += kPlanThreads)
+        A.row_ok[j] = 0;
+    if (tid == 0)
+        *A.err = 0;
+    __syncthreads();
+    // segments [s0, s1) of this thread, in order
+    const int per = (nb + kPlanThreads - 1) / kPlanThreads;
+    const int s0 = min(nb, tid * per), s1 = min(nb, s0 + per);
+    int cnt[4] = {0, 0, 0, 0};
+    for (int i = s0; i < s1; ++i) {
+        const int e = A.eids[i];
+        const char *blob = (e >= 0 && e < A.n_table) ? static_cast<const char *>(A.table[e])
+                                                     : nullptr;
+        if (reinterpret_cast<uintptr_t>(blob) & 255) {  // not a slab / tier blob address
+            *A.err = 2;
+            blob = nullptr;
+        }
+        const int x0 = A.xoff[i];
+        int n = A.nr[i];
+        if (x0 < 0 || x0 > nrows)
+            n = 0;
+        n = max(0, min(n, nrows - max(x0, 0)));
+        ExpertWork w{};
+        if (blob) {
+            w.w[0] = blob + A.off[0];
+            w.s[0] = blob + A.off[1];
+            w.w[1] = blob + A.off[2];
+            w.s[1] = blob + A.off[3];
+            w.w[2] = blob + A.off[4];
+            w.s[2] = blob + A.off[5];
+        }
+        w.row0 = max(x0, 0);
+        w.nrows = blob ? n : 0;
+        A.ew[i] = w;
+        if (!blob || n == 0)
+            continue;
+        for (int j = x0; j < x0 + n; ++j)
+            A.row_ok[j] = 1;
+        cnt[A.top] += n / A.bm;
+        if (n % A.bm)
+            cnt[dplan_class(n % A.bm)] += 1;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        part[tid][c] = cnt[c];
+    __syncthreads();
+    // exclusive scan over threads, one class per wave of the first four
+    if (tid < 4 * 64) {
+        const int c = tid >> 6, l = tid & 63;
+        constexpr int kPer = kPlanThreads / 64;  // 16 consecutive threads per lane
+        int run = 0;
+        for (int k = 0; k < kPer; ++k) {
+            const int v = part[l * kPer + k][c];
+            part[l * kPer + k][c] = run;
+            run += v;
+        }
+        // exclusive scan of the lanes' sums
+        int incl = run;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (l >= o)
+                incl += v;
+        }
+        const int base = incl - run;
+        for (int k = 0; k < kPer; ++k)
+            part[l * kPer + k][c] += base;
+        if (l == 63)
+            tot[c] = incl;
+    }
+    __syncthreads();
+    int pos[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        pos[c] = part[tid][c];
+    for (int i = s0; i < s1; ++i) {
+        const ExpertWork &w = A.ew[i];
+        const int n = w.nrows;
+        for (int r0 = 0; r0 < n; r0 += A.bm) {
+            const int nrow = min(A.bm, n - r0);
+            const int c = nrow == A.bm ? A.top : dplan_class(nrow);
+            if (pos[c] < A.item_cap[c])
+                A.items[A.item_base[c] + pos[c]] = int4{i, r0, nrow, 0};
+            else
+                *A.err = 1;
+            ++pos[c];
+        }
+    }
+    if (tid < 4)
+        A.n_items[tid] = min(tot[tid], A.item_cap[tid]);
+}
+
+// ---- the combine lists -----------------------------------------------------------
+
+__device__ __forceinline__ int csr_live(const CsrArgs &A, int j) {
+    const int t = A.rows[j];
+    return (A.row_ok[j] && t >= 0 && t < A.S) ? t : -1;
+}
+
+__global__ void k_csr_zero(CsrArgs A) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t <= A.S; t += gridDim.x * blockDim.x)
+        A.cnt[t] = 0;
+}
+
+__global__ void k_csr_count(CsrArgs A) {
+    const int n = min(max(A.counts[1], 0), A.cap_rows);
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+        const int t = csr_live(A, j);
+        if (t >= 0)
+            atomicAdd(&A.cnt[t], 1);
+    }
+}
+
+// exclusive scan of cnt[0..S) into cnt[0..S] (tok_ptr) and cursor, one workgroup
+__global__ __launch_bounds__(kPlanThreads) void k_csr_scan(CsrArgs A) {
+    __shared__ int wsum[kPlanThreads / 64];
+    __shared__ int carry;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0)
+        carry = 0;
+    __syncthreads();
+    for (int b = 0; b < A.S; b += kPlanThreads) {
+        const int t = b + tid;
+        const int v = t < A.S ? A.cnt[t] : 0;
+        int incl = v;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(incl, o);
+            if (lane >= o)
+                incl += u;
+        }
+        if (lane == 63)
+            wsum[wave] = incl;
+        __syncthreads();
+        int before = carry;
+        for (int w = 0; w < wave; ++w)
+            before += wsum[w];
+        const int excl = before + incl - v;
+        __syncthreads();  // every thread has read carry and wsum
+        if (t < A.S) {
+            A.cnt[t] = excl;
+            A.cursor[t] = excl;
+        }
+        if (tid == kPlanThreads - 1)
+            carry = excl + v;
+        __syncthreads();
+    }
+    if (tid == 0)
+        A.cnt[A.S] = carry;
+}
+
+__global__ void k_csr_place(CsrArgs A) {
+    const int n = min(max(A.counts[1], 0), A.cap_rows);
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < n; j += gridDim.x * blockDim.x) {
+        const int t = csr_live(A, j);
+        if (t < 0)
+            continue;
+        const int p = atomicAdd(&A.cursor[t], 1);
+        A.ent_row[p] = j;
+        A.ent_w[p] = A.rw[j];
+    }
+}
+
+// each out row's entries in ascending compact row (insertion sort: a row has about top-k
+// entries)
+__global__ void k_csr_sort(CsrArgs A) {
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < A.S; t += gridDim.x * blockDim.x) {
+        const int e0 = A.cnt[t], e1 = A.cnt[t + 1];
+        for (int i = e0 + 1; i < e1; ++i) {
+            const int r = A.ent_row[i];
+            const float w = A.ent_w[i];
+            int k = i - 1;
+            while (k >= e0 && A.ent_row[k] > r) {
+                A.ent_row[k + 1] = A.ent_row[k];
+                A.ent_w[k + 1] = A.ent_w[k];
+                --k;
+            }
+            A.ent_row[k + 1] = r;
+            A.ent_w[k + 1] = w;
+        }
+    }
+}
+
+hipError_t launch_dplan(const DPlanArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_dplan, dim3(1), dim3(kPlanThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_dcsr(const CsrArgs &a, hipStream_t st) {
+    const unsigned gs = (unsigned)std::min(1024, (a.S + 255) / 256 + 1);
+    const unsigned gr = (unsigned)std::min(1024, (a.cap_rows + 255) / 256);
+    hipLaunchKernelGGL(k_csr_zero, dim3(gs), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_csr_count, dim3(gr), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_csr_scan, dim3(1), dim3(kPlanThreads), 0, st, a);
+    hipLaunchKernelGGL(k_csr_place, dim3(gr), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(k_csr_sort, dim3(gs), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+}  // namespace mvllm_hip

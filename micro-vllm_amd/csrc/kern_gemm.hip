@@ -45,6 +45,8 @@ struct GemmArgs {
     float *out;         // single: Y [rcap][O] f32
     int nbn;            // column blocks per item
     int n_tasks;        // items * nbn
+    const int *n_items_dev;  // non-null: the item count is in device memory (a grid sized
+                             // for its bound; workgroups past items * nbn exit)
     int xcd;            // 1: tasks ordered per XCD (xcd_task), 0: task = workgroup index
     int K, O, rcap;
     int act;
@@ -107,7 +109,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int K = A.K, O = A.O, rcap = A.rcap;
-    const int n_tasks = A.n_tasks;
+    const int n_tasks =
+        A.n_items_dev ? __builtin_amdgcn_readfirstlane(*A.n_items_dev) * A.nbn : A.n_tasks;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63, t = lane & 15, q = lane >> 4;
@@ -429,12 +432,20 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
 // issued first (clamped to the row, so they stay unconditional; only the stores are).
 constexpr int kPrepThreads = 256, kPrepUnroll = 4;
 
+// n_live (device, may be null): rows j >= *n_live are left alone (a grid sized for a
+// bound).  src_rows >= 0: a source row outside [0, src_rows) gives a zero row.
 template <int FMT, int TERMS>
 __global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
                                                               const int *rows_map, int K,
-                                                              int rcap, __bf16 *planes) {
+                                                              int rcap, __bf16 *planes,
+                                                              const int *n_live, int src_rows) {
     const int j = blockIdx.x;
-    const int src = rows_map ? rows_map[j] : j;
+    if (n_live && j >= *n_live)
+        return;
+    int src = rows_map ? rows_map[j] : j;
+    const bool zero = src_rows >= 0 && (src < 0 || src >= src_rows);
+    if (zero)
+        src = 0;
     const int per_row = K >> 3;
     const float4 *p = reinterpret_cast<const float4 *>(x + (size_t)src * K);
     for (int c0 = 0; c0 < per_row; c0 += kPrepUnroll * kPrepThreads) {
@@ -444,6 +455,8 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
             const int c = min(c0 + u * kPrepThreads + (int)threadIdx.x, per_row - 1);
             v[u][0] = p[2 * c];
             v[u][1] = p[2 * c + 1];
+            if (zero)
+                v[u][0] = v[u][1] = float4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int u = 0; u < kPrepUnroll; ++u) {
@@ -524,7 +537,7 @@ static hipError_t launch_gemm_fd(const GemmArgs &a, int n_items, int terms, int 
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act,
-                       float act_a, float act_b, hipStream_t st) {
+                       float act_a, float act_b, hipStream_t st, const int *n_items_dev) {
     if (n_items <= 0)
         return hipSuccess;
     if (K % kGemmBK || O % (dual ? 128 : 256) || gemm_lds_bytes(fmt, terms, mt) > 163840)
@@ -542,6 +555,7 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
     a.act = act;
     a.act_a = act_a;
     a.act_b = act_b;
+    a.n_items_dev = n_items_dev;
     if (fmt == 4)
         return dual ? launch_gemm_fd<4, true>(a, n_items, terms, mt, st)
                     : launch_gemm_fd<4, false>(a, n_items, terms, mt, st);
@@ -583,7 +597,8 @@ hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, i
 }
 
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
-                              int K, int rcap, void *planes, hipStream_t st) {
+                              int K, int rcap, void *planes, hipStream_t st, const int *n_live,
+                              int src_rows) {
     if (R <= 0)
         return hipSuccess;
     if (K % 8)
@@ -591,7 +606,7 @@ hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *row
     __bf16 *pl = static_cast<__bf16 *>(planes);
 #define MVLLM_PREP(F, T)                                                                      \
     hipLaunchKernelGGL((k_prep_planes<F, T>), dim3((unsigned)R), dim3(kPrepThreads), 0, st, x, \
-                       rows_map, K, rcap, pl)
+                       rows_map, K, rcap, pl, n_live, src_rows)
     if (fmt == 4) {
         if (terms == 1) MVLLM_PREP(4, 1); else if (terms == 2) MVLLM_PREP(4, 2); else MVLLM_PREP(4, 3);
     } else if (fmt == 7) {

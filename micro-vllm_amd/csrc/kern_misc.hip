@@ -15,7 +15,7 @@ __global__ __launch_bounds__(64) void k_combine(CombineArgs A) {
 #pragma clang fp contract(off)
     const int t = blockIdx.y;
     const int e0 = A.tok_ptr[t], e1 = A.tok_ptr[t + 1];
-    float *orow = A.out + (size_t)A.out_row[t] * (size_t)A.D;
+    float *orow = A.out + (size_t)(A.out_row ? A.out_row[t] : t) * (size_t)A.D;
     if ((A.D & 3) == 0 && ((uintptr_t)A.out & 15) == 0) {
         const int d4 = blockIdx.x * 64 + threadIdx.x;
         if (d4 * 4 >= A.D)

@@ -38,7 +38,7 @@ struct CombineArgs {
     const int *tok_ptr;
     const int *ent_row;
     const float *ent_w;
-    const int *out_row;
+    const int *out_row;  // null: out row t
     float *out;
     int n_tok, D;
 };
@@ -158,13 +158,14 @@ bool gemm_xcd();
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act, float act_a, float act_b,
-                       hipStream_t st);
+                       hipStream_t st, const int *n_items_dev = nullptr);
 // One matrix (w[2], s[2] of *ew1) over input rows [0, nrows) of the planes, in items of
 // 16 * mt rows computed in the kernel (a dense linear): out [nrows][O] f32.
 hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, int nrows,
                             const void *pin, float *out, int K, int O, hipStream_t st);
 hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *rows_map, int R,
-                              int K, int rcap, void *planes, hipStream_t st);
+                              int K, int rcap, void *planes, hipStream_t st,
+                              const int *n_live = nullptr, int src_rows = -1);
 
 // f32-weight GEMMs on the matrix cores (kern_f32.hip): fmt 0 moe_block, router scores,
 // fmt 0 linears.  Items {expert, r0, nrow, 0} of <= 16 * mt rows (mt 1, 2, 4), or, with
@@ -197,5 +198,43 @@ hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *
                            int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,
                            float *out, int K, int O, int rcap, int act, float act_a, float act_b,
                            hipStream_t st);
+
+// ---- device-planned calls (kern_dplan.hip) ---------------------------------------
+
+// k_dplan: expert work, row liveness and grouped-GEMM items of a call whose segments are
+// in device memory.
+struct DPlanArgs {
+    const void *const *table;  // blob address per expert id (device)
+    int n_table;
+    long long off[6];  // piece offsets: gate_p gate_s up_p up_s down_p down_s
+    const int *counts;  // [0] segments, [1] compact rows
+    const int *eids, *xoff, *nr;
+    int cap_e, cap_rows;
+    int bm;            // rows per full block (16 * top class)
+    int top;           // index of the top class (log2 of its MT)
+    ExpertWork *ew;    // [cap_e]
+    int4 *items;       // class c at items + item_base[c] ({expert, r0, nrow, 0})
+    int item_base[4], item_cap[4];
+    int *n_items;      // [4]
+    unsigned char *row_ok;  // [cap_rows]
+    int *err;          // 0; 1 = a class overflowed its capacity (the bounds exclude it),
+                       // 2 = a blob address not 256-byte aligned (that expert skipped)
+};
+
+// The combine's per-out-row lists of such a call (tok_ptr in cnt after the scan).
+struct CsrArgs {
+    const int *counts;  // [1] compact rows
+    int cap_rows, S;
+    const int *rows;
+    const float *rw;
+    const unsigned char *row_ok;
+    int *cnt;      // [S + 1]: per out row, then (after the scan) tok_ptr
+    int *cursor;   // [S]
+    int *ent_row;  // [cap_rows]
+    float *ent_w;  // [cap_rows]
+};
+
+hipError_t launch_dplan(const DPlanArgs &a, hipStream_t st);
+hipError_t launch_dcsr(const CsrArgs &a, hipStream_t st);
 
 }  // namespace mvllm_hip

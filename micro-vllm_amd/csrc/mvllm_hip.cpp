@@ -24,6 +24,10 @@
 #include <unordered_map>
 #include <vector>
 
+namespace mvllm_hip {
+void set_error(const std::string &s);
+}
+
 using namespace mvllm_hip;
 
 namespace {
@@ -50,6 +54,13 @@ bool in_one_host_block(const uint8_t *lo, const uint8_t *hi) {
 }
 
 void set_err(const std::string &s) { g_err = s; }
+
+}  // namespace
+
+// the library's other host files report through the same thread's error text
+void mvllm_hip::set_error(const std::string &s) { set_err(s); }
+
+namespace {
 
 #define HIP_TRY(expr)                                                                         \
     do {                                                                                      \
@@ -160,6 +171,7 @@ struct Ctx {
     bool have_last = false;
     DevBuf H, Y, Xc, Oc, miss, Ph, HP, Xp;
     DevBuf Lp;  // planes of mvllm_hip_linear_dev's input rows
+    DevBuf Rp;  // device plan of mvllm_hip_moe_block_routed_dev
     HostBuf hx, ho;
     // Plan slots, reused in groups of kGroup: one event after a group's last call guards
     // the reuse of all its slots.  A group whose last call did not reach finish_call is
@@ -1205,6 +1217,7 @@ void mvllm_hip_shutdown(void) {
     C.HP.release();
     C.Xp.release();
     C.Lp.release();
+    C.Rp.release();
     C.Xc.release();
     C.Oc.release();
     C.miss.release();
@@ -1721,6 +1734,118 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
     }
     HIP_TRY(launch_moe_route(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, rows, rw,
                              cap_experts, cap_rows, counts, static_cast<hipStream_t>(stream)));
+    return 1;
+}
+
+int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const *table,
+                                   int n_table, const int *counts, const int *eids,
+                                   const int *xoff, const int *nr, int cap_experts,
+                                   const int *rows, const float *rw, int cap_rows,
+                                   const float *x, float *out, int S, int act, float act_a,
+                                   float act_b, int *status, void *stream) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    HostClock hc(&C.stats[15]);
+    set_err("");
+    if (!C.ready || !table || n_table < 1 || !counts || !eids || !xoff || !nr || !rows || !rw ||
+        !x || !out || cap_experts < 1 || cap_rows < 1 || S < 1 || S > 65535 ||
+        (fmt != 4 && fmt != 7) || D < 256 || D % 256 || Iinter < 256 || Iinter % 256 ||
+        !aligned(x, 16) || (long long)cap_rows * D > (1ll << 31)) {
+        set_err("moe_block_routed_dev: bad arguments (fmt 4/7, D and Iinter multiples of 256, "
+                "1 <= S <= 65535, caps >= 1, x 16-byte aligned)");
+        return 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // bf16 terms per activation: two (2^-17 relative, the decode accuracy) for calls of at
+    // most 256 rows, one (the prefill arithmetic) above; mode 1 always two, mode 2 one
+    const int terms = C.mode == 1 ? 2 : C.mode == 2 ? 1 : (cap_rows <= 256 ? 2 : 1);
+    const int max_mt = gemm_max_mt(fmt, terms);
+    const int top = max_mt == 8 ? 3 : 2, bm = 16 * max_mt;
+    // items per class at most: one remainder per expert of >= lo rows; the top class's
+    // items (full blocks and remainders above bm / 2) hold >= lo[top] rows each
+    static const int lo[4] = {1, 17, 33, 65};
+    int cap[4] = {0, 0, 0, 0}, base[4] = {0, 0, 0, 0}, n_it = 0;
+    for (int c = 0; c <= top; ++c) {
+        if (cap_rows >= lo[c])
+            cap[c] = c == top ? cap_rows / lo[c] : std::min(cap_experts, cap_rows / lo[c]);
+        base[c] = n_it;
+        n_it += cap[c];
+    }
+    long long off6[6];
+    (void)mvllm_expert_geom(fmt, D, Iinter, off6);
+    auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
+    const size_t b_ew = al((size_t)cap_experts * sizeof(ExpertWork)), b_it = al((size_t)n_it * 16);
+    const size_t b_misc = 256, b_ok = al((size_t)cap_rows), b_cnt = al(((size_t)S + 1) * 4);
+    const size_t b_cur = al((size_t)S * 4), b_er = al((size_t)cap_rows * 4);
+    const size_t total = b_ew + b_it + b_misc + b_ok + b_cnt + b_cur + 2 * b_er;
+    if (!order_after_previous(C, st))
+        return 0;
+    HIP_TRY(C.Rp.ensure(total));
+    HIP_TRY(C.Xp.ensure((size_t)terms * cap_rows * D * 2));
+    HIP_TRY(C.Ph.ensure((size_t)terms * cap_rows * Iinter * 2));
+    HIP_TRY(C.Y.ensure((size_t)cap_rows * D * 4));
+    char *p = static_cast<char *>(C.Rp.p);
+    DPlanArgs a{};
+    a.table = table;
+    a.n_table = n_table;
+    for (int k = 0; k < 6; ++k)
+        a.off[k] = off6[k];
+    a.counts = counts;
+    a.eids = eids;
+    a.xoff = xoff;
+    a.nr = nr;
+    a.cap_e = cap_experts;
+    a.cap_rows = cap_rows;
+    a.bm = bm;
+    a.top = top;
+    a.ew = reinterpret_cast<ExpertWork *>(p);
+    a.items = reinterpret_cast<int4 *>(p + b_ew);
+    for (int c = 0; c < 4; ++c) {
+        a.item_base[c] = base[c];
+        a.item_cap[c] = cap[c];
+    }
+    char *misc = p + b_ew + b_it;
+    a.n_items = reinterpret_cast<int *>(misc);
+    a.err = status ? status : reinterpret_cast<int *>(misc + 64);
+    a.row_ok = reinterpret_cast<unsigned char *>(misc + b_misc);
+    CsrArgs cs{};
+    cs.counts = counts;
+    cs.cap_rows = cap_rows;
+    cs.S = S;
+    cs.rows = rows;
+    cs.rw = rw;
+    cs.row_ok = a.row_ok;
+    cs.cnt = reinterpret_cast<int *>(misc + b_misc + b_ok);
+    cs.cursor = reinterpret_cast<int *>(misc + b_misc + b_ok + b_cnt);
+    cs.ent_row = reinterpret_cast<int *>(misc + b_misc + b_ok + b_cnt + b_cur);
+    cs.ent_w = reinterpret_cast<float *>(misc + b_misc + b_ok + b_cnt + b_cur + b_er);
+    HIP_TRY(launch_dplan(a, st));
+    HIP_TRY(launch_prep_planes(fmt, terms, x, rows, cap_rows, D, cap_rows, C.Xp.p, st,
+                               counts + 1, S));
+    for (int c = 0; c <= top; ++c)
+        if (cap[c])
+            HIP_TRY(launch_gemm(fmt, true, terms, 1 << c, a.ew, a.items + base[c], cap[c], C.Xp.p,
+                                C.Ph.p, nullptr, D, Iinter, cap_rows, act, act_a, act_b, st,
+                                a.n_items + c));
+    for (int c = 0; c <= top; ++c)
+        if (cap[c])
+            HIP_TRY(launch_gemm(fmt, false, terms, 1 << c, a.ew, a.items + base[c], cap[c],
+                                C.Ph.p, nullptr, static_cast<float *>(C.Y.p), Iinter, D,
+                                cap_rows, 0, 0.f, 0.f, st, a.n_items + c));
+    HIP_TRY(launch_dcsr(cs, st));
+    CombineArgs cb{};
+    cb.Y = static_cast<const float *>(C.Y.p);
+    cb.tok_ptr = cs.cnt;
+    cb.ent_row = cs.ent_row;
+    cb.ent_w = cs.ent_w;
+    cb.out_row = nullptr;
+    cb.out = out;
+    cb.n_tok = S;
+    cb.D = D;
+    HIP_TRY(launch_combine(cb, st));
+    C.stats[0] += 1;
+    C.last_stream = st;
+    C.have_last = true;
     return 1;
 }
 

@@ -68,6 +68,13 @@ _SIGS = {
     "mvllm_hip_moe_route_dev": (_i, [_p, _p, _i, _i, _i, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i,
                                      _p, _p]),
     "mvllm_hip_membench": (_i, [_i, _p, _p, _sz, _i, _i, _p]),
+    "mvllm_st_expert_pieces": (_i, [C.c_char_p, C.c_char_p, _i, _i, _i, _i, _i, _i, _p, _p, _p,
+                                    _p, _ll, _p, _ll]),
+    "mvllm_hip_slab_load": (_ll, [C.c_char_p, C.c_char_p, _i, _i, _i, _i, _i, _i]),
+    "mvllm_hip_slab_info": (_i, [_ll, _pp, _pp, _p, _p, _p]),
+    "mvllm_hip_slab_free": (_i, [_ll]),
+    "mvllm_hip_moe_block_routed_dev": (_i, [_i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _p, _p, _i,
+                                            _p, _p, _i, _i, _f, _f, _p, _p]),
 }
 
 _lib = None
@@ -264,6 +271,18 @@ def moe_route_dev(choice, mix, n_tok, n_exp, k, idx, wt, work, eids, xoff, nr, r
                                          _stream(stream)), "mvllm_hip_moe_route_dev")
 
 
+def moe_block_routed_dev(D, Iinter, fmt, table, n_table, counts, eids, xoff, nr, rows, rw, x,
+                         out, S, act=ACT_SILU, act_a=0.0, act_b=0.0, status=None, stream=None):
+    """mvllm_hip_moe_block_routed_dev: segments (counts, eids, xoff, nr, rows, rw) and the
+    blob table in device memory; caps are the lengths of eids and rows.  Enqueued."""
+    _check(lib().mvllm_hip_moe_block_routed_dev(D, Iinter, fmt, _ptr(table), n_table,
+                                                _ptr(counts), _ptr(eids), _ptr(xoff), _ptr(nr),
+                                                len(eids), _ptr(rows), _ptr(rw), len(rows),
+                                                _ptr(x), _ptr(out), S, act, act_a, act_b,
+                                                _ptr(status), _stream(stream)),
+           "mvllm_hip_moe_block_routed_dev")
+
+
 def router_dev(x, w, bias, n_tok, D, n_exp, k, rscale, scores, choice, idx, wt, stream=None):
     """cpu_route of every token row on the device (see mvllm_hip_router_dev); enqueued."""
     _check(lib().mvllm_hip_router_dev(_ptr(x), _ptr(w), _ptr(bias), n_tok, D, n_exp, k, rscale,
@@ -298,3 +317,51 @@ def membench(kind, src, dst, nbytes, row_bytes=0, reps=5):
     _check(lib().mvllm_hip_membench(kind, _ptr(src), _ptr(dst), nbytes, row_bytes, reps,
                                     _ptr(ms)), "mvllm_hip_membench")
     return float(ms[0])
+
+
+def st_expert_pieces(dirpath, prefix, fmt, D, Iinter, layer0, layer1, n_experts):
+    """-> (paths, file [n, 6], offset [n, 6], bytes [n, 6]) for n = (layer1 - layer0) *
+    n_experts blobs; raises HipError with the reference's message when a piece is missing
+    or has the wrong size (see mvllm_st_expert_pieces).  Host only."""
+    n = (layer1 - layer0) * n_experts * 6
+    fi = np.zeros(max(n, 1), np.int32)
+    off = np.zeros(max(n, 1), np.int64)
+    nb = np.zeros(max(n, 1), np.int64)
+    paths = C.create_string_buffer(1 << 16)
+    err = C.create_string_buffer(1024)
+    r = lib().mvllm_st_expert_pieces(dirpath.encode(), (prefix or "").encode(), fmt, D, Iinter,
+                                     layer0, layer1, n_experts, _ptr(fi), _ptr(off), _ptr(nb),
+                                     C.cast(paths, C.c_void_p), len(paths),
+                                     C.cast(err, C.c_void_p), len(err))
+    if r < 0:
+        raise HipError(err.value.decode())
+    files = [p for p in paths.value.decode().split("\n") if p]
+    return files, fi[:n].reshape(-1, 6), off[:n].reshape(-1, 6), nb[:n].reshape(-1, 6)
+
+
+class Slab:
+    """A layer range of routed experts read from safetensors containers into HBM (see
+    mvllm_hip_slab_load).  .base / .table are device addresses, .stride the blob stride."""
+
+    def __init__(self, dirpath, prefix, fmt, D, Iinter, layer0, layer1, n_experts):
+        h = lib().mvllm_hip_slab_load(dirpath.encode(), (prefix or "").encode(), fmt, D, Iinter,
+                                      layer0, layer1, n_experts)
+        if h <= 0:
+            raise HipError("mvllm_hip_slab_load failed: " + lib().mvllm_hip_last_error().decode())
+        self.handle = h
+        base, table = C.c_void_p(), C.c_void_p()
+        stride, blob, nbl = np.zeros(1, np.int64), np.zeros(1, np.int64), np.zeros(1, np.int32)
+        _check(lib().mvllm_hip_slab_info(h, C.byref(base), C.byref(table), _ptr(stride),
+                                         _ptr(blob), _ptr(nbl)), "mvllm_hip_slab_info")
+        self.base, self.table = base.value, table.value
+        self.stride, self.blob_bytes, self.n_blobs = int(stride[0]), int(blob[0]), int(nbl[0])
+        self.fmt, self.D, self.I = fmt, D, Iinter
+        self.layer0, self.n_experts = layer0, n_experts
+
+    def blob(self, layer, e):
+        return self.base + ((layer - self.layer0) * self.n_experts + e) * self.stride
+
+    def free(self):
+        if self.handle:
+            _check(lib().mvllm_hip_slab_free(self.handle), "mvllm_hip_slab_free")
+            self.handle = 0

@@ -1,0 +1,188 @@
+"""The device-resident layer (mvllm_hip_moe_block_routed_dev): routing on the device, then
+the block on the segments where the routing left them, experts resolved through a device
+blob table; no host round trip (src/model/glm53.cpp:1938-1992 with the device route).
+
+Checked against
+  * the host-planned call on the same segments (read back) with the same arithmetic
+    (grouped GEMM, same bf16 terms): bit for bit, since items compute rows independently
+    and both combines sum in the reference's expert order;
+  * the oracle's host chain (moe_topk per token, moe_segments, moe_block) within the
+    arithmetic's bar: 2e-5 for two bf16 terms per activation, 1e-2 (the north-star bar for
+    bf16 outputs) for one.
+Also: null and out-of-table experts consume their rows without writing, and calls whose
+caps exceed the routed sizes (surplus workgroups exit) give the same bits.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import npref
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def layer(hip, fmt, D, I, T, E, k, seed, null_ids=(), routing="uniform"):
+    from mvllm_hip import synth
+    rng = np.random.default_rng(seed)
+    geom = hip.expert_geom(fmt, D, I)
+    pool, stride = synth.device_pool(torch, fmt, D, I, E, seed, geom)
+    X = rng.standard_normal((T, D)).astype(np.float32)
+    if routing == "skewed":  # a few hot experts: segments of many rows
+        bias = np.zeros(E, np.float32)
+        bias[:3] = 4.0
+        choice = (rng.standard_normal((T, E)) + bias).astype(np.float32)
+    else:
+        choice = rng.standard_normal((T, E)).astype(np.float32)
+    mix = (1 / (1 + np.exp(-choice))).astype(np.float32)
+    table = np.array([pool.data_ptr() + e * stride for e in range(E)], np.uint64)
+    for e in null_ids:
+        table[e] = 0
+    return rng, pool, stride, geom, X, choice, mix, table
+
+
+def route(hip, choice, mix, k, cap_rows=None, cap_e=None):
+    T, E = choice.shape
+    i32 = dict(dtype=torch.int32, device="cuda")
+    idx, wt = torch.empty((T, k), **i32), torch.empty((T, k), dtype=torch.float32, device="cuda")
+    work, counts = torch.zeros(2 * E + 1, **i32), torch.empty(2, **i32)
+    ce, cr = cap_e or E, cap_rows or T * k
+    eids, xoff, nr = (torch.zeros(ce, **i32) for _ in range(3))
+    rows, rw = torch.zeros(cr, **i32), torch.zeros(cr, dtype=torch.float32, device="cuda")
+    hip.moe_route_dev(dev(choice), dev(mix), T, E, k, idx, wt, work, eids, xoff, nr, rows, rw,
+                      counts)
+    return counts, eids, xoff, nr, rows, rw
+
+
+def run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b):
+    counts, eids, xoff, nr, rows, rw = seg
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    status = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    hip.moe_block_routed_dev(D, I, fmt, dev(table.view(np.int64)), len(table), counts, eids,
+                             xoff, nr, rows, rw, dev(X), out, T, act, a, b, status=status)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), int(status.cpu()[0])
+
+
+def host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, act, a, b, table):
+    counts, eids, xoff, nr, rows, rw = seg
+    nb, n = (int(v) for v in counts.cpu().numpy())
+    g_eids, g_xoff, g_nr = (t.cpu().numpy()[:nb] for t in (eids, xoff, nr))
+    g_rows, g_rw = rows.cpu().numpy()[:n], rw.cpu().numpy()[:n]
+    off = geom[1]
+    order = (0, 2, 4, 1, 3, 5)
+    ptrs = [[(int(table[e]) + int(off[o])) if table[e] else None for e in g_eids]
+            for o in order]
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    hip.moe_block_dev(nb, D, I, fmt, *ptrs, dev(X[g_rows]), g_xoff, g_nr, g_rows, g_rw, out, T,
+                      act, a, b)
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), (nb, g_eids, g_xoff, g_nr, g_rows, g_rw)
+
+
+def oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, act, a, b,
+                 null_ids=()):
+    from mvllm_hip import synth
+    E = choice.shape[1]
+    hi = np.zeros((T, k), np.int32)
+    hw = np.zeros((T, k), np.float32)
+    for t in range(T):
+        _, hi[t], hw[t] = orc.moe_topk(choice[t], k, mix[t])
+    enb, e_eids, e_xoff, e_nr, e_rows, e_rw = orc.moe_segments(hi, hw, T, k, E)
+    blobs = {int(e): pool[int(e)].cpu().numpy() for e in e_eids}
+    lists = [[], [], [], [], [], []]
+    for e in e_eids:
+        pieces = synth.blob_pieces(blobs[int(e)], fmt, D, I, geom[1])
+        for j in range(6):
+            lists[j].append(None if int(e) in null_ids else pieces[j])
+    exp = np.zeros((T, D), np.float32)
+    assert orc.moe_block(enb, D, I, fmt, *lists, X[e_rows], e_xoff, e_nr, e_rows, e_rw, exp, T,
+                         act, a, b) == 1
+    return exp
+
+
+CASES = [
+    # fmt, D, I, T, E, k, routing
+    (7, 1024, 512, 6, 48, 4, "uniform"),      # decode-like: <= 256 rows, two terms
+    (4, 512, 256, 16, 64, 8, "uniform"),
+    (7, 512, 256, 300, 64, 8, "skewed"),      # > 256 rows: one term; hot experts of many rows
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_routed_block(hip, orc, case):
+    fmt, D, I, T, E, k, routing = case
+    say("routed block", case)
+    from mvllm_hip import ACT_CLAMP_SWIGLU, ACT_SITU
+    act, a, b = (ACT_CLAMP_SWIGLU, 7.0, 0.0) if fmt == 4 else (ACT_SITU, 4.0, 25.0)
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 17 + T,
+                                                          routing=routing)
+    seg = route(hip, choice, mix, k)
+    got, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)
+    assert status == 0
+    two_terms = T * k <= 256
+    # the host-planned call with the same arithmetic: grouped GEMM, same terms
+    hip.set_option("gemm", 1)
+    hip.set_option("mode", 1 if two_terms else 0)
+    try:
+        ref, info = host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, act, a, b, table)
+    finally:
+        hip.set_option("gemm", 0)
+        hip.set_option("mode", 0)
+    nb, _, _, g_nr, _, _ = info
+    say(f"  segments {nb}, rows {int(g_nr.sum())}, largest {int(g_nr.max())}")
+    if routing == "skewed":
+        assert int(g_nr.max()) > 64  # the top row class runs
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    exp = oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, act, a, b)
+    err = npref.rel_err(got, exp)
+    say("  rel_err vs oracle chain", err)
+    assert err < (2e-5 if two_terms else 1e-2)
+
+
+def test_routed_block_null_and_missing_experts(hip, orc):
+    fmt, D, I, T, E, k = 7, 512, 256, 12, 32, 4
+    from mvllm_hip import ACT_SITU
+    null_ids = (0, 5, 9)
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 99,
+                                                          null_ids=null_ids)
+    seg = route(hip, choice, mix, k)
+    # the table covers only experts [0, E - 4): the last four are outside it
+    short = table[:E - 4]
+    got, status = run_routed(hip, fmt, D, I, short, seg, X, T, ACT_SITU, 4.0, 25.0)
+    assert status == 0
+    gone = set(null_ids) | set(range(E - 4, E))
+    exp = oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, ACT_SITU, 4.0,
+                       25.0, null_ids=gone)
+    err = npref.rel_err(got, exp)
+    say("null / missing experts: rel_err", err)
+    assert err < 2e-5
+    # a misaligned blob address is skipped and reported
+    bad = table.copy()
+    bad[1] += 16
+    got2, status2 = run_routed(hip, fmt, D, I, bad, seg, X, T, ACT_SITU, 4.0, 25.0)
+    assert status2 == 2
+
+
+def test_routed_block_surplus_caps(hip):
+    """Caps above the routed sizes (the grid sized for them, surplus workgroups exit) give
+    the same bits as exact caps."""
+    fmt, D, I, T, E, k = 4, 512, 256, 40, 64, 8
+    from mvllm_hip import ACT_CLAMP_SWIGLU
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 5)
+    a = run_routed(hip, fmt, D, I, table, route(hip, choice, mix, k), X, T, ACT_CLAMP_SWIGLU,
+                   7.0, 0.0)[0]
+    b = run_routed(hip, fmt, D, I, table, route(hip, choice, mix, k, cap_rows=T * k + 200,
+                                                cap_e=E + 50), X, T, ACT_CLAMP_SWIGLU, 7.0,
+                   0.0)[0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
