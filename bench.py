@@ -224,6 +224,8 @@ def main():
     ap.add_argument("--probe-sizes", action="store_true",
                     help="also time the stream-read probe at launch-sized reads (8 MiB .. "
                          "1 GiB, each repetition at a new offset of the pool)")
+    ap.add_argument("--pipeline", action="store_true",
+                    help="only the c2 layer pipeline (HBM tier fed like the store feeds it)")
     ap.add_argument("--staged", type=float, default=None, metavar="MISS_RATE",
                     help="only the drop-in host entry with the HBM expert tier: this fraction "
                          "of each step's experts is copied from pinned host memory by the call")
@@ -248,6 +250,10 @@ def main():
         k, v = kv.split("=", 1)
         if not mvllm_hip.set_option(k, int(v)):
             raise SystemExit(f"option {kv} refused")
+    if args.pipeline:
+        print(json.dumps(layer_pipeline(np, torch, mvllm_hip, synth,
+                                        dict(synth.CONFIGS["c2"]))), flush=True)
+        return
     if args.staged is not None:
         print(json.dumps(staged(args, np, torch, mvllm_hip, synth, cfg, T, args.steps,
                                 args.warmup, args.staged,
@@ -291,6 +297,8 @@ def main():
             torch.cuda.empty_cache()
         extra["c2 T=1 staged"] = staged(args, np, torch, mvllm_hip, synth,
                                         dict(synth.CONFIGS["c2"]), 1, 50, 5, 0.25, 0.0)
+        extra["c2 layer pipeline"] = layer_pipeline(np, torch, mvllm_hip, synth,
+                                                    dict(synth.CONFIGS["c2"]))
         route, scores = route_timing(torch, mvllm_hip, 2048, 384, 8)
         if not args.no_cpu:
             route["cpu_us_per_call"], route["cpu_kind"] = cpu_route_baseline(np, scores, 8)
@@ -490,6 +498,143 @@ def staged(args, np, torch, mvllm_hip, synth, cfg, T, steps, warmup, miss_rate, 
     del pool
     torch.cuda.empty_cache()
     return rec
+
+
+def layer_pipeline(np, torch, mvllm_hip, synth, cfg, n_layers=12, steps=4, miss_rate=0.25):
+    """The GPU-resident decode of one token through n_layers MoE layers of config c2, the
+    HBM tier fed from a pinned RAM tier the way the store feeds it: per layer, routing
+    (uniform top-k) picks nb experts, round(miss_rate * nb) of which are not in HBM; they
+    are staged with mvllm_hip_prefetch from pinned host blobs, the layer's blob table
+    comes from mvllm_hip_tier_table (its stream waits for the copies) and the block runs
+    with mvllm_hip_moe_block_routed_dev on segments in device memory.  After each step the
+    missed experts are evicted, so every step misses again.
+      serialized: layer l's misses staged, then layer l computed, then the host waits
+                  (so layer l + 1's copies cannot start during layer l's compute);
+      pipelined:  layer l + 1's misses staged while layer l computes (the store's
+                  prefetch of the next layer);
+      copy only / compute only: the two halves alone.
+    Overlap = (serialized - pipelined) / min(copy, compute) per layer."""
+    import ctypes
+    D, I, fmt, E, k = cfg["D"], cfg["I"], cfg["fmt"], cfg["E"], cfg["k"]
+    nbytes, off = mvllm_hip.expert_geom(fmt, D, I)
+    stride = (nbytes + 4095) // 4096 * 4096
+    rng = np.random.default_rng(77)
+    nb = k  # T = 1: one token's k experts
+    n_miss = int(round(miss_rate * nb))
+    eids = [np.sort(rng.choice(E, size=nb, replace=False)) for _ in range(n_layers)]
+    miss = [list(rng.choice(e, size=n_miss, replace=False)) for e in eids]
+    # pinned RAM tier: every routed expert of every layer (the resident ones are promoted
+    # from it at set-up)
+    L = mvllm_hip.lib()
+    n_blobs = n_layers * nb
+    host = L.mvllm_hip_host_alloc(n_blobs * stride)
+    if not host:
+        raise SystemExit("pinned host allocation failed")
+    pool, _, _, _ = build_pool(torch, mvllm_hip, fmt, D, I, nb, 4321)
+    slot = {}
+    for l in range(n_layers):
+        for j, e in enumerate(eids[l]):
+            b = l * nb + j
+            slot[(l, int(e))] = host + b * stride
+            src = pool[j, :nbytes].cpu().numpy()  # nb distinct blobs, reused across layers
+            ctypes.memmove(host + b * stride, src.ctypes.data, nbytes)
+    del pool
+    torch.cuda.empty_cache()
+    for l in range(n_layers):
+        for e in eids[l]:
+            if e not in miss[l]:
+                mvllm_hip.promote(slot[(l, int(e))], nbytes, l, int(e))
+    torch.cuda.synchronize()
+    # per layer: segments (one token, weights normalized) and x, in device memory
+    i32 = dict(dtype=torch.int32, device="cuda")
+    segs = []
+    for l in range(n_layers):
+        w = rng.uniform(0.1, 1.0, nb).astype(np.float32)
+        w /= w.sum()
+        segs.append((torch.tensor([nb, nb], **i32), torch.tensor(eids[l].astype(np.int32), **i32),
+                     torch.arange(nb, **i32), torch.ones(nb, **i32), torch.zeros(nb, **i32),
+                     torch.from_numpy(w).cuda()))
+    x = torch.from_numpy(rng.standard_normal((1, D)).astype(np.float32)).cuda()
+    out = torch.zeros((1, D), dtype=torch.float32, device="cuda")
+    table = torch.zeros(E, dtype=torch.int64, device="cuda")
+
+    def stage(l):
+        ms = miss[l]
+        mvllm_hip.prefetch([l] * len(ms), ms, [slot[(l, int(e))] for e in ms], [nbytes] * len(ms))
+
+    def compute(l):
+        mvllm_hip.tier_table(l, E, table)
+        c, e_, xo, nr_, rows, rw = segs[l]
+        mvllm_hip.moe_block_routed_dev(D, I, fmt, table, E, c, e_, xo, nr_, rows, rw, x, out, 1,
+                                       cfg["act"], cfg["a"], cfg["b"])
+        mvllm_hip.tier_table_done(l)
+
+    def unstage():
+        for l in range(n_layers):
+            for e in miss[l]:
+                mvllm_hip.evict(l, int(e))
+
+    def run(kind):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        total = 0.0
+        for s in range(steps + 1):
+            torch.cuda.synchronize()
+            e0.record()
+            if kind == "pipelined":
+                stage(0)
+                for l in range(n_layers):
+                    compute(l)
+                    if l + 1 < n_layers:
+                        stage(l + 1)
+            else:
+                for l in range(n_layers):
+                    if kind in ("serialized", "copy"):
+                        stage(l)
+                    if kind in ("serialized", "compute"):
+                        compute(l)
+                    if kind == "serialized":  # the next copies start after this compute
+                        torch.cuda.synchronize()
+            if kind == "copy":  # the copies end on the copy stream: order the end event
+                mvllm_hip.tier_table(0, E, table)
+            e1.record()
+            torch.cuda.synchronize()
+            if s > 0:  # the first pass warms up
+                total += e0.elapsed_time(e1)
+            if kind != "compute":
+                unstage()
+        return total / steps / n_layers * 1e3  # us per layer
+
+    # compute only: every expert resident
+    for l in range(n_layers):
+        stage(l)
+    torch.cuda.synchronize()
+    t_compute = run("compute")
+    unstage()
+    torch.cuda.synchronize()
+    t_copy = run("copy")
+    t_ser = run("serialized")
+    t_pipe = run("pipelined")
+    mvllm_hip.tier_table(0, E, table)
+    torch.cuda.synchronize()
+    for l in range(n_layers):
+        for e in eids[l]:
+            mvllm_hip.evict(l, int(e))
+    L.mvllm_hip_host_free(host)
+    staged_mb = n_miss * nbytes / 1e6
+    overlap = (t_ser - t_pipe) / max(min(t_copy, t_compute), 1e-9)
+    log(f"layer pipeline c2 ({n_layers} layers, {n_miss} of {nb} experts staged per layer, "
+        f"{staged_mb:.1f} MB): per layer copy {t_copy:.1f} us ({staged_mb / t_copy * 1e3:.1f} "
+        f"GB/s), compute {t_compute:.1f} us, serialized {t_ser:.1f} us, pipelined "
+        f"{t_pipe:.1f} us: overlap {overlap:.2f} of the shorter half")
+    return {"workload": f"c2 {cfg['desc']}, T=1, {n_layers} layers, {n_miss} of {nb} experts "
+                        "per layer staged from pinned host memory (mvllm_hip_prefetch), blocks "
+                        "on device-resident segments (mvllm_hip_moe_block_routed_dev)",
+            "us_per_layer": {"copy_only": round(t_copy, 2), "compute_only": round(t_compute, 2),
+                             "serialized": round(t_ser, 2), "pipelined": round(t_pipe, 2)},
+            "staged_mb_per_layer": round(staged_mb, 2),
+            "h2d_gbps": round(staged_mb / t_copy * 1e3, 2),
+            "overlap_of_shorter_half": round(overlap, 3),
+            "value": round(1e6 / (t_pipe * n_layers), 3), "unit": "tokens/s (12 layers)"}
 
 
 def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):

@@ -313,6 +313,42 @@ int mvllm_hip_evict(int layer, int eid);
 /* Device address of a resident blob (NULL if absent); waits for its copy. */
 void *mvllm_hip_resident_ptr(int layer, int eid);
 
+/* The store's prefetch path (ExpertStore::prefetch / prefetch_one_async,
+ * src/store/expert_store.cpp:73-91, 416-456): n blobs (layers[i], eids[i]) that the RAM
+ * tier holds at host_blobs[i] (bytes[i]) start their copies into HBM on the copy stream,
+ * as mvllm_hip_promote, without waiting; resident ones only move up the LRU.  A layer's
+ * experts prefetched while the previous layer computes are in HBM when its block runs.
+ * Returns the number of copies enqueued, or -1 (see mvllm_hip_last_error). */
+int mvllm_hip_prefetch(int n, const int *layers, const int *eids, const void *const *host_blobs,
+                       const size_t *bytes);
+
+/* The store's REPIN path (ExpertStore::take_repin, src/store/expert_store.cpp:305-316,
+ * 524-538): the RAM tier evicted these experts (layer_eid = n pairs layer, eid), so their
+ * host slots now hold other experts.  Their HBM copies stay resident (reachable by
+ * (layer, eid): mvllm_hip_resident_ptr, mvllm_hip_tier_table) but host pointers no longer
+ * map to them.  Returns how many resident blobs were unlinked, or -1. */
+int mvllm_hip_repin(int n, const int *layer_eid);
+
+/* The store's slot reuse (ExpertStore::load_into evicting a slot for another expert,
+ * src/store/expert_store.cpp:300-318): call before the slot [host_lo, host_lo + bytes)
+ * is rewritten.  Waits until every promotion copy from that range has finished, then
+ * unlinks the HBM blobs mapped to it as mvllm_hip_repin does.  Returns the number
+ * unlinked, or -1.  (The moe_block host entry's own miss copies finish before it
+ * returns.) */
+int mvllm_hip_host_reuse(const void *host_lo, size_t bytes);
+
+/* A layer's blob table for mvllm_hip_moe_block_routed_dev: table_dev[e] (device array of
+ * n_experts entries) = the HBM address of resident (layer, e) or NULL, written on
+ * `stream`, which first waits for every promotion enqueued so far (so prefetched experts
+ * are complete when the block reads them).  *n_resident (may be NULL) = entries that are
+ * not NULL.  Blobs of the layer are not recycled before mvllm_hip_tier_table_done(layer,
+ * stream) has been called after the compute that reads the table.  n_experts <= 8192.
+ * 1 ok. */
+int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resident,
+                         void *stream);
+/* Marks the end of the layer's table readers on `stream` (see above).  1 ok. */
+int mvllm_hip_tier_table_done(int layer, void *stream);
+
 /* Counters since init (or the last reset): index
  *  0 moe_block calls      1 rows computed        2 H2D bytes (weights)
  *  3 H2D bytes (acts/out) 4 D2H bytes            5 promotions

@@ -197,6 +197,16 @@ struct Ctx {
     std::map<const uint8_t *, long long> by_host;  // host blob start -> key
     std::list<long long> lru;                      // front = most recent
     std::multimap<size_t, void *> free_blocks;     // recycled device blocks by size
+    // per layer: the end of the last compute that read a tier table of it
+    // (mvllm_hip_tier_table_done); a blob of the layer is recycled only after it
+    std::unordered_map<int, hipEvent_t> layer_use;
+    // pinned staging of tier tables, a ring guarded by one event per entry
+    static constexpr int kTabSlots = 8, kTabMax = 8192;
+    HostBuf tab_host[kTabSlots];
+    hipEvent_t tab_done[kTabSlots] = {};
+    bool tab_used[kTabSlots] = {};
+    int tab_next = 0;
+    hipEvent_t tier_ready = nullptr;  // copy stream: every promotion enqueued so far
     std::vector<std::pair<size_t, void *>> pending_free;
     // stats
     double stats[17] = {0};
@@ -1140,9 +1150,13 @@ void res_drop(Ctx &C, long long key) {
     // stream waits for the last reader before writing into a recycled block
     if (r.used)
         (void)hipStreamWaitEvent(C.copy, r.last_use, 0);
+    auto lu = C.layer_use.find(r.layer);
+    if (lu != C.layer_use.end())
+        (void)hipStreamWaitEvent(C.copy, lu->second, 0);
     C.free_blocks.emplace(r.bytes, r.dev);
     C.used_bytes -= r.bytes;
-    C.by_host.erase(r.host);
+    if (r.host)
+        C.by_host.erase(r.host);
     C.lru.erase(r.lru);
     (void)hipEventDestroy(r.ready);
     (void)hipEventDestroy(r.last_use);
@@ -1195,6 +1209,13 @@ int mvllm_hip_init(int device) {
         HIP_TRY(hipEventCreateWithFlags(&e, kEvFlags));
     HIP_TRY(hipEventCreateWithFlags(&C.prev_done, kEvFlags));
     HIP_TRY(hipEventCreateWithFlags(&C.miss_done, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&C.tier_ready, kEvFlags));
+    for (int i = 0; i < Ctx::kTabSlots; ++i) {
+        HIP_TRY(C.tab_host[i].ensure(Ctx::kTabMax * sizeof(void *)));
+        HIP_TRY(hipEventCreateWithFlags(&C.tab_done[i], kEvFlags));
+        C.tab_used[i] = false;
+    }
+    C.tab_next = 0;
     C.device = device;
     C.ready = true;
     return 1;
@@ -1242,6 +1263,16 @@ void mvllm_hip_shutdown(void) {
     C.prev_done = nullptr;
     (void)hipEventDestroy(C.miss_done);
     C.miss_done = nullptr;
+    (void)hipEventDestroy(C.tier_ready);
+    C.tier_ready = nullptr;
+    for (auto &lu : C.layer_use)
+        (void)hipEventDestroy(lu.second);
+    C.layer_use.clear();
+    for (int i = 0; i < Ctx::kTabSlots; ++i) {
+        C.tab_host[i].release();
+        (void)hipEventDestroy(C.tab_done[i]);
+        C.tab_done[i] = nullptr;
+    }
     for (void *p : g_retired)
         (void)hipFree(p);
     g_retired.clear();
@@ -1557,10 +1588,15 @@ int mvllm_hip_set_expert_budget(size_t bytes) {
     return 1;
 }
 
-int mvllm_hip_promote(const void *host_blob, size_t bytes, int layer, int eid) {
-    Ctx &C = ctx();
-    std::lock_guard<std::mutex> lk(C.mu);
-    set_err("");
+}  // extern "C"
+
+namespace {
+
+// One promotion (mvllm_hip_promote / mvllm_hip_prefetch); *staged = 1 when a copy was
+// enqueued, 0 when the blob was resident already.  Caller holds C.mu.
+int promote_locked(Ctx &C, const void *host_blob, size_t bytes, int layer, int eid,
+                   int *staged) {
+    *staged = 0;
     if (!C.ready || !host_blob || bytes == 0) {
         set_err("promote: not initialised or empty blob");
         return 0;
@@ -1614,6 +1650,139 @@ int mvllm_hip_promote(const void *host_blob, size_t bytes, int layer, int eid) {
     C.used_bytes += bytes;
     C.stats[5] += 1;
     C.stats[2] += static_cast<double>(bytes);
+    *staged = 1;
+    return 1;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mvllm_hip_promote(const void *host_blob, size_t bytes, int layer, int eid) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    int staged;
+    return promote_locked(C, host_blob, bytes, layer, eid, &staged);
+}
+
+int mvllm_hip_prefetch(int n, const int *layers, const int *eids, const void *const *host_blobs,
+                       const size_t *bytes) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (n < 0 || (n > 0 && (!layers || !eids || !host_blobs || !bytes))) {
+        set_err("prefetch: bad arguments");
+        return -1;
+    }
+    int count = 0;
+    for (int i = 0; i < n; ++i) {
+        int staged;
+        if (!promote_locked(C, host_blobs[i], bytes[i], layers[i], eids[i], &staged))
+            return -1;
+        count += staged;
+    }
+    return count;
+}
+
+int mvllm_hip_repin(int n, const int *layer_eid) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (n < 0 || (n > 0 && !layer_eid)) {
+        set_err("repin: bad arguments");
+        return -1;
+    }
+    int count = 0;
+    for (int i = 0; i < n; ++i) {
+        auto it = C.res.find(res_key(layer_eid[2 * i], layer_eid[2 * i + 1]));
+        if (it == C.res.end() || !it->second.host)
+            continue;
+        // the host slot now belongs to another expert: the HBM copy stays, addressable by
+        // (layer, eid), but no host pointer maps to it any more
+        C.by_host.erase(it->second.host);
+        it->second.host = nullptr;
+        ++count;
+    }
+    return count;
+}
+
+int mvllm_hip_host_reuse(const void *host_lo, size_t bytes) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !host_lo || bytes == 0) {
+        set_err("host_reuse: bad arguments");
+        return -1;
+    }
+    const uint8_t *lo = static_cast<const uint8_t *>(host_lo), *hi = lo + bytes;
+    int count = 0;
+    for (auto h = C.by_host.begin(); h != C.by_host.end();) {
+        Resident &r = C.res[h->second];
+        if (r.host < hi && lo < r.host + r.bytes) {
+            // the copy from the old contents must be complete before the slot is rewritten
+            if (hipEventSynchronize(r.ready) != hipSuccess) {
+                set_err("host_reuse: hipEventSynchronize failed");
+                return -1;
+            }
+            r.host = nullptr;
+            h = C.by_host.erase(h);
+            ++count;
+        } else {
+            ++h;
+        }
+    }
+    return count;
+}
+
+int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resident,
+                         void *stream) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready || !table_dev || n_experts < 1 || n_experts > Ctx::kTabMax) {
+        set_err("tier_table: bad arguments (1 <= n_experts <= 8192)");
+        return 0;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int si = C.tab_next;
+    C.tab_next = (si + 1) % Ctx::kTabSlots;
+    if (C.tab_used[si])
+        HIP_TRY(hipEventSynchronize(C.tab_done[si]));
+    void **h = static_cast<void **>(C.tab_host[si].p);
+    int count = 0;
+    for (int e = 0; e < n_experts; ++e) {
+        auto it = C.res.find(res_key(layer, e));
+        h[e] = it == C.res.end() ? nullptr : it->second.dev;
+        if (h[e]) {
+            C.lru.splice(C.lru.begin(), C.lru, it->second.lru);
+            ++count;
+        }
+    }
+    // the compute that reads the table runs after every promotion enqueued so far
+    HIP_TRY(hipEventRecord(C.tier_ready, C.copy));
+    HIP_TRY(hipStreamWaitEvent(st, C.tier_ready, 0));
+    HIP_TRY(hipMemcpyAsync(table_dev, h, (size_t)n_experts * sizeof(void *),
+                           hipMemcpyHostToDevice, st));
+    HIP_TRY(hipEventRecord(C.tab_done[si], st));
+    C.tab_used[si] = true;
+    if (n_resident)
+        *n_resident = count;
+    return 1;
+}
+
+int mvllm_hip_tier_table_done(int layer, void *stream) {
+    Ctx &C = ctx();
+    std::lock_guard<std::mutex> lk(C.mu);
+    set_err("");
+    if (!C.ready) {
+        set_err("tier_table_done: not initialised");
+        return 0;
+    }
+    hipEvent_t &ev = C.layer_use[layer];
+    if (!ev)
+        HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming | hipEventDisableSystemFence));
+    HIP_TRY(hipEventRecord(ev, static_cast<hipStream_t>(stream)));
     return 1;
 }
 

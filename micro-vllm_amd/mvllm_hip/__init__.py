@@ -73,6 +73,11 @@ _SIGS = {
     "mvllm_hip_slab_load": (_ll, [C.c_char_p, C.c_char_p, _i, _i, _i, _i, _i, _i]),
     "mvllm_hip_slab_info": (_i, [_ll, _pp, _pp, _p, _p, _p]),
     "mvllm_hip_slab_free": (_i, [_ll]),
+    "mvllm_hip_prefetch": (_i, [_i, _p, _p, _pp, _p]),
+    "mvllm_hip_repin": (_i, [_i, _p]),
+    "mvllm_hip_host_reuse": (_i, [_p, _sz]),
+    "mvllm_hip_tier_table": (_i, [_i, _i, _p, _p, _p]),
+    "mvllm_hip_tier_table_done": (_i, [_i, _p]),
     "mvllm_hip_moe_block_routed_dev": (_i, [_i, _i, _i, _p, _i, _p, _p, _p, _p, _i, _p, _p, _i,
                                             _p, _p, _i, _i, _f, _f, _p, _p]),
 }
@@ -365,3 +370,34 @@ class Slab:
         if self.handle:
             _check(lib().mvllm_hip_slab_free(self.handle), "mvllm_hip_slab_free")
             self.handle = 0
+
+
+def prefetch(layers, eids, host_blobs, nbytes):
+    """mvllm_hip_prefetch: -> copies enqueued."""
+    n = len(eids)
+    la, ea = np.asarray(layers, np.int32), np.asarray(eids, np.int32)
+    by = np.asarray(nbytes, np.uint64)
+    r = lib().mvllm_hip_prefetch(n, _ptr(la), _ptr(ea), _ptr_array(list(host_blobs)), _ptr(by))
+    if r < 0:
+        raise HipError("mvllm_hip_prefetch failed: " + lib().mvllm_hip_last_error().decode())
+    return r
+
+
+def repin(pairs):
+    a = np.asarray(pairs, np.int32).reshape(-1, 2)
+    r = lib().mvllm_hip_repin(len(a), _ptr(a))
+    if r < 0:
+        raise HipError("mvllm_hip_repin failed: " + lib().mvllm_hip_last_error().decode())
+    return r
+
+
+def tier_table(layer, n_experts, table_dev, stream=None):
+    """-> number of resident entries written into table_dev (enqueued on stream)."""
+    nres = np.zeros(1, np.int32)
+    _check(lib().mvllm_hip_tier_table(layer, n_experts, _ptr(table_dev), _ptr(nres),
+                                      _stream(stream)), "mvllm_hip_tier_table")
+    return int(nres[0])
+
+
+def tier_table_done(layer, stream=None):
+    _check(lib().mvllm_hip_tier_table_done(layer, _stream(stream)), "mvllm_hip_tier_table_done")
