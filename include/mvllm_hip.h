@@ -341,8 +341,10 @@ int mvllm_hip_host_reuse(const void *host_lo, size_t bytes);
  * n_experts entries) = the HBM address of resident (layer, e) or NULL, written on
  * `stream`, which first waits for every promotion enqueued so far (so prefetched experts
  * are complete when the block reads them).  *n_resident (may be NULL) = entries that are
- * not NULL.  Blobs of the layer are not recycled before mvllm_hip_tier_table_done(layer,
- * stream) has been called after the compute that reads the table.  n_experts <= 8192.
+ * not NULL.  Each table is closed by one mvllm_hip_tier_table_done(layer, stream) after
+ * the compute that reads it: until the layer's last open table is closed, a blob of the
+ * layer that is dropped meanwhile (evicted by a concurrent promotion) keeps its device
+ * block, and a later copy into the block waits for those readers.  n_experts <= 8192.
  * 1 ok. */
 int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resident,
                          void *stream);

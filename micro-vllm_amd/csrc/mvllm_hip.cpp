@@ -200,6 +200,11 @@ struct Ctx {
     // per layer: the end of the last compute that read a tier table of it
     // (mvllm_hip_tier_table_done); a blob of the layer is recycled only after it
     std::unordered_map<int, hipEvent_t> layer_use;
+    // per layer: tables handed out and not yet closed by mvllm_hip_tier_table_done, and
+    // the blocks of the layer's blobs dropped meanwhile (their readers may still be
+    // unrecorded: the blocks are recycled when the last open table is closed)
+    std::unordered_map<int, int> layer_open;
+    std::unordered_map<int, std::vector<std::pair<size_t, void *>>> layer_parked;
     // pinned staging of tier tables, a ring guarded by one event per entry
     static constexpr int kTabSlots = 8, kTabMax = 8192;
     HostBuf tab_host[kTabSlots];
@@ -1153,7 +1158,11 @@ void res_drop(Ctx &C, long long key) {
     auto lu = C.layer_use.find(r.layer);
     if (lu != C.layer_use.end())
         (void)hipStreamWaitEvent(C.copy, lu->second, 0);
-    C.free_blocks.emplace(r.bytes, r.dev);
+    auto lo = C.layer_open.find(r.layer);
+    if (lo != C.layer_open.end() && lo->second > 0)
+        C.layer_parked[r.layer].emplace_back(r.bytes, r.dev);
+    else
+        C.free_blocks.emplace(r.bytes, r.dev);
     C.used_bytes -= r.bytes;
     if (r.host)
         C.by_host.erase(r.host);
@@ -1232,6 +1241,11 @@ void mvllm_hip_shutdown(void) {
     for (auto &fb : C.free_blocks)
         (void)hipFree(fb.second);
     C.free_blocks.clear();
+    for (auto &lp : C.layer_parked)
+        for (auto &fb : lp.second)
+            (void)hipFree(fb.second);
+    C.layer_parked.clear();
+    C.layer_open.clear();
     C.H.release();
     C.Y.release();
     C.Ph.release();
@@ -1766,6 +1780,7 @@ int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resi
                            hipMemcpyHostToDevice, st));
     HIP_TRY(hipEventRecord(C.tab_done[si], st));
     C.tab_used[si] = true;
+    C.layer_open[layer] += 1;
     if (n_resident)
         *n_resident = count;
     return 1;
@@ -1783,6 +1798,17 @@ int mvllm_hip_tier_table_done(int layer, void *stream) {
     if (!ev)
         HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming | hipEventDisableSystemFence));
     HIP_TRY(hipEventRecord(ev, static_cast<hipStream_t>(stream)));
+    int &open = C.layer_open[layer];
+    open = open > 0 ? open - 1 : 0;
+    auto lp = C.layer_parked.find(layer);
+    if (open == 0 && lp != C.layer_parked.end() && !lp->second.empty()) {
+        // blobs of the layer dropped while its tables were open: copies into their
+        // blocks wait for the readers recorded just now
+        HIP_TRY(hipStreamWaitEvent(C.copy, ev, 0));
+        for (auto &fb : lp->second)
+            C.free_blocks.emplace(fb.first, fb.second);
+        lp->second.clear();
+    }
     return 1;
 }
 

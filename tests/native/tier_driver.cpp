@@ -7,7 +7,9 @@
 // from (layer, eid), as a pread would bring it), calling mvllm_hip_host_reuse before it
 // rewrites a slot and queueing the evicted expert as a REPIN event; prefetch() loads the
 // next layer's experts and hands them to mvllm_hip_prefetch (the store's
-// prefetch_one_async path).  Slots are pinned by leases while a call reads them.
+// prefetch_one_async path).  Slots are pinned by leases while a call or a prefetch reads
+// them, and a slot being loaded is handed to no one until its load ends (the store's
+// loading state).
 //
 //   store thread:   for each layer l + 1 ahead of the compute thread: prefetch its
 //                   experts; drain REPIN events into mvllm_hip_repin.
@@ -79,9 +81,11 @@ struct RamTier {
     struct Slot {
         uint8_t *base = nullptr;
         int eid = -1, pins = 0;
+        bool loading = false;
         unsigned long long used = 0;
     };
     std::mutex mu;
+    std::condition_variable loaded;
     std::vector<std::vector<Slot>> layers;
     std::deque<std::pair<int, int>> repin;
     unsigned long long clock = 1;
@@ -102,25 +106,36 @@ struct RamTier {
             for (auto &s : L)
                 mvllm_hip_host_free(s.base);
     }
-    // the slot holding (layer, eid), loading it when absent; pinned when pin
+    // the slot holding (layer, eid), loading it when absent; leased when pin (release()
+    // ends the lease).  A slot that another thread is loading is waited for.
     uint8_t *lookup(int layer, int eid, bool pin) {
         std::unique_lock<std::mutex> lk(mu);
         auto &L = layers[layer];
-        for (auto &s : L)
-            if (s.eid == eid) {
-                s.used = clock++;
-                s.pins += pin;
-                return s.base;
+        for (;;) {
+            Slot *hit = nullptr;
+            for (auto &s : L)
+                if (s.eid == eid)
+                    hit = &s;
+            if (!hit)
+                break;
+            if (hit->loading) {
+                loaded.wait(lk);
+                continue;  // the slot may have changed hands meanwhile
             }
+            hit->used = clock++;
+            hit->pins += pin;
+            return hit->base;
+        }
         Slot *v = nullptr;
         for (auto &s : L)
-            if (s.pins == 0 && (!v || s.used < v->used))
+            if (s.pins == 0 && !s.loading && (!v || s.used < v->used))
                 v = &s;
         if (!v)
             return nullptr;  // every slot leased
         const int old = v->eid;
         v->eid = eid;
         v->used = clock++;
+        v->loading = true;
         v->pins += 1;  // held during the load
         lk.unlock();
         // the slot is about to be rewritten: copies from its old contents must finish
@@ -129,10 +144,12 @@ struct RamTier {
         reuse_calls++;
         fill_blob(v->base, layer, eid);
         lk.lock();
+        v->loading = false;
         v->pins -= 1;
         v->pins += pin;
         if (old >= 0)
             repin.emplace_back(layer, old);
+        loaded.notify_all();
         return v->base;
     }
     void release(uint8_t *base) {
@@ -427,8 +444,10 @@ int main(int argc, char **argv) {
             std::vector<int> ls, es;
             std::vector<const void *> hb;
             std::vector<size_t> by;
+            // leased until the promotions are enqueued: the compute thread may not
+            // rewrite a slot between its load and the copy out of it
             for (int i = 0; i < c.nb; ++i) {
-                uint8_t *p = ram.lookup(layer, c.eids[i], false);
+                uint8_t *p = ram.lookup(layer, c.eids[i], true);
                 if (!p)
                     continue;
                 ls.push_back(layer);
@@ -441,6 +460,8 @@ int main(int argc, char **argv) {
                 std::fprintf(stderr, "prefetch: %s\n", mvllm_hip_last_error());
                 failures++;
             }
+            for (const void *p : hb)
+                ram.release(static_cast<uint8_t *>(const_cast<void *>(p)));
             std::vector<int> rp = ram.take_repin();
             if (mvllm_hip_repin((int)rp.size() / 2, rp.data()) < 0)
                 failures++;
@@ -468,6 +489,11 @@ int main(int argc, char **argv) {
         std::vector<const float *> gs(c.nb), us(c.nb), ds(c.nb);
         for (int i = 0; i < c.nb; ++i) {
             lease[i] = ram.lookup(layer, c.eids[i], true);
+            // the store's leases are short (until its promotions are enqueued)
+            for (int tries = 0; !lease[i] && tries < 20000; ++tries) {
+                usleep(100);
+                lease[i] = ram.lookup(layer, c.eids[i], true);
+            }
             if (!lease[i]) {
                 std::fprintf(stderr, "all slots leased\n");
                 return 2;
