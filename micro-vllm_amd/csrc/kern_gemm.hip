@@ -53,6 +53,9 @@ struct GemmArgs {
     float act_a, act_b;
 };
 
+#ifndef MVLLM_PIPE_A
+#define MVLLM_PIPE_A 1
+#endif
 constexpr int kGemmThreads = 512;
 constexpr int kGemmBK = 256;
 constexpr int kGemmPitch = kGemmBK * 2 + 16;  // LDS bytes per A row and plane (+16: banks)
@@ -105,6 +108,9 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     constexpr int PL = BM * kGemmPitch;                  // bytes per plane per stage
     constexpr int STAGE = gemm_stage_bytes(FMT, TERMS, MT);
     constexpr int ACH = TERMS * BM * (kGemmBK / 8) / kGemmThreads;  // 16-byte chunks/thread
+    // Row tiles' A fragments read one tile ahead where registers allow (the one-workgroup
+    // classes: their MFMAs otherwise wait out each tile's LDS latency)
+    constexpr bool kPipeA = MVLLM_PIPE_A && MT >= 4 && TERMS == 1;
     static_assert(ACH * kGemmThreads == TERMS * BM * (kGemmBK / 8), "A staging split");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -259,15 +265,33 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
                     exc |= (uint32_t)b7_exceptional(sg[m]);
                 }
             }
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
+            // A fragments of row tile mt (two 32-wide halves of group g, per term)
+            auto read_a = [&] __attribute__((always_inline)) (int mt, bf16x8 (&a)[TERMS][2]) {
                 const char *ap = base + (mt * 16 + t) * kGemmPitch + (64 * g + 16 * q) * 2;
-                bf16x8 a[TERMS][2];
 #pragma unroll
                 for (int tm = 0; tm < TERMS; ++tm)
 #pragma unroll
                     for (int s = 0; s < 2; ++s)
                         a[tm][s] = *reinterpret_cast<const bf16x8 *>(ap + tm * PL + 16 * s);
+            };
+            bf16x8 an[TERMS][2];
+            if constexpr (kPipeA)
+                read_a(0, an);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                bf16x8 a[TERMS][2];
+                if constexpr (kPipeA) {
+                    // the next row tile's fragments are read before this tile's MFMAs, so
+                    // their LDS latency runs under the MFMAs
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; ++tm)
+                        a[tm][0] = an[tm][0], a[tm][1] = an[tm][1];
+                    if (mt + 1 < MT)
+                        read_a(mt + 1, an);
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    read_a(mt, a);
+                }
                 if constexpr (FMT == 4) {
                     // each 64-wide group is its own chain over n - 8, then one f32 FMA
                     // applies the group's scale
@@ -301,7 +325,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
                                                                                  acc[mt][m], 0, 0, 0);
                         }
                 }
-                // one row tile's A fragments live at a time (register pressure)
+                // one row tile's A fragments live at a time, or two with kPipeA
+                // (register pressure)
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
