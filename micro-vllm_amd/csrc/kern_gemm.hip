@@ -53,6 +53,9 @@ struct GemmArgs {
     float act_a, act_b;
 };
 
+#ifndef MVLLM_CHUNK_S
+#define MVLLM_CHUNK_S 1
+#endif
 #ifndef MVLLM_PIPE_A
 #define MVLLM_PIPE_A 1
 #endif
@@ -86,6 +89,19 @@ struct GScale {
     uint32_t s7[FMT == 7 ? 2 : 1];
 };
 
+// Scales in chunks of 64 bytes of each row (MXFP4: four pairs of steps, int4: two): lane
+// 4 r + c holds bytes 64 C + 16 c .. + 15 of row r, i.e. MXFP4 pair 4 C + c whole, or
+// int4 groups 16 C + 4 c .. + 3.  One load per chunk instead of per pair: a row's scale
+// line is fetched from HBM about twice, where per-pair loads far apart in time fetched it
+// again after each L2 eviction (the small-expert classes read ~25 % more than their
+// weights and scales).
+struct GScaleC {
+    u32x4 c[2];
+};
+// pairs of K steps per scale chunk
+template <int FMT>
+__host__ __device__ constexpr int gscale_ppc() { return FMT == 7 ? 4 : 2; }
+
 // Where one task's operands live: its two weight tiles (buffer resources + this lane's
 // offsets), its activation rows and its output columns.
 template <int FMT>
@@ -103,6 +119,12 @@ struct TaskD {
 template <int FMT, bool DUAL, int TERMS, int MT, bool UNI>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
+    // scales in 64-byte chunks (GScaleC) where the registers allow
+    // (not the MXFP4 down kernel of the 16-row class: it would pass 128 VGPRs)
+    constexpr bool kChunkS =
+        MVLLM_CHUNK_S && !UNI && (MT == 4 || (MT == 1 && (DUAL || FMT == 4)));
+    constexpr int PPC = gscale_ppc<FMT>();
+    using Scl = std::conditional_t<kChunkS, GScaleC, GScale<FMT>>;
     constexpr int BM = 16 * MT;
     constexpr int PA = MT >= 8 ? 1 : 2;  // activation prefetch distance in K steps
     constexpr int PL = BM * kGemmPitch;                  // bytes per plane per stage
@@ -147,7 +169,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             d.rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
             d.rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
             d.vw[m] = (uint32_t)(trow + (lane >> 2)) * rowb + 8u * (uint32_t)(lane & 3);
-            d.vs[m] = (uint32_t)(trow + (lane >> 2)) * srow + (FMT == 4 ? 8u : 4u) * (uint32_t)(lane & 3);
+            d.vs[m] = (uint32_t)(trow + (lane >> 2)) * srow +
+                      (kChunkS ? 16u : FMT == 4 ? 8u : 4u) * (uint32_t)(lane & 3);
         }
         return d;
     };
@@ -161,16 +184,28 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
                     u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rw[m], d.vw[m] + 32 * g,
                                                                 (uint32_t)k * 128u, 0));
     };
-    // scales of the pair holding step k
-    auto load_s = [&] __attribute__((always_inline)) (GScale<FMT> &s, const TaskD<FMT> &d, int k) {
-        const uint32_t off = (uint32_t)(k >> 1) * (FMT == 4 ? 32u : 16u);
+    // scales of the pair holding step k; chunked: the chunk holding step k, loaded only
+    // when step k opens the chunk (otherwise the offset lies past the buffer, which loads
+    // zeros without touching memory and keeps the body free of branches)
+    auto load_s = [&] __attribute__((always_inline)) (Scl &s, const TaskD<FMT> &d, int k) {
+        if constexpr (kChunkS) {
+            const bool open = ((k >> 1) % PPC) == 0;
+            const uint32_t off = (uint32_t)((k >> 1) / PPC) * 64u;
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-            if constexpr (FMT == 4)
-                s.s4[m] = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rs[m], d.vs[m], off, 0));
-            else
-                s.s7[m] = __builtin_amdgcn_raw_buffer_load_b32(d.rs[m], d.vs[m], off, 0);
+            for (int m = 0; m < 2; ++m)
+                s.c[m] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               d.rs[m], open ? d.vs[m] + off : 0xffffff00u, 0, 0));
+        } else {
+            const uint32_t off = (uint32_t)(k >> 1) * (FMT == 4 ? 32u : 16u);
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+                if constexpr (FMT == 4)
+                    s.s4[m] = __builtin_bit_cast(
+                        u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rs[m], d.vs[m], off, 0));
+                else
+                    s.s7[m] = __builtin_amdgcn_raw_buffer_load_b32(d.rs[m], d.vs[m], off, 0);
+            }
         }
     };
 
@@ -216,13 +251,16 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     const int src4 = 4 * (4 * t + q);  // ds_bpermute address of lane 4 t + q
 
 
-    // step j (0 or 1) of the pair whose scales are sc
+    // step j (0 or 1) of pair p, whose scales are in sc
     auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf,
-                                                         const GScale<FMT> &sc, int j, auto exact) {
+                                                         const Scl &sc, int p, int j, auto exact) {
         constexpr bool EXACT = decltype(exact)::value;
         const char *base = smem + buf * STAGE;
-        // scale words of step j, groups 0-1 / 2-3, sit in lanes 4 t + 2 j and 4 t + 2 j + 1
-        const int ssrc = 4 * (4 * t + 2 * j);
+        // scale words of step j, groups 0-1 / 2-3, sit in lanes 4 t + 2 j and 4 t + 2 j + 1;
+        // chunked: MXFP4 pair p in lane 4 t + p % 4 (word 2 j + g / 2), int4 groups of step
+        // j in lane 4 t + 2 (p % 2) + j (component g)
+        const int ssrc = kChunkS ? (FMT == 7 ? 4 * (4 * t + p % PPC) : 4 * (4 * t + 2 * (p % PPC) + j))
+                                 : 4 * (4 * t + 2 * j);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             bf16x8 bf[2][2];
@@ -232,7 +270,15 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             for (int m = 0; m < 2; ++m) {
                 const uint32_t wx = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].x);
                 const uint32_t wy = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].y);
-                if constexpr (FMT == 4) {
+                if constexpr (kChunkS && FMT == 4) {
+                    sg[m] = __uint_as_float(
+                        (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc, (int)sc.c[m][g]));
+                } else if constexpr (kChunkS) {
+                    const uint32_t word = (uint32_t)__builtin_amdgcn_ds_bpermute(
+                        ssrc, (int)sc.c[m][2 * j + (g >> 1)]);
+                    const int byte = 2 * (g & 1) + (q >> 1);
+                    sg[m] = __uint_as_float(((word >> (8 * byte)) & 0xffu) << 23);
+                } else if constexpr (FMT == 4) {
                     sg[m] = __uint_as_float((uint32_t)__builtin_amdgcn_ds_bpermute(
                         ssrc + 4 * (g >> 1), (int)((g & 1) ? sc.s4[m].y : sc.s4[m].x)));
                 } else {  // lanes q < 2 take 32-block 2 g, q >= 2 block 2 g + 1
@@ -373,7 +419,7 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     const int task = A.xcd ? xcd_task(blockIdx.x, n_tasks) : (int)blockIdx.x;
     const TaskD<FMT> cur = make_task(task);
     GStep<FMT> b0, b1;
-    GScale<FMT> sc, sn;  // scales of this pair of steps / of the next pair
+    Scl sc, sn;  // scales of this pair of steps (chunk) / of the next pair (chunk)
     AStage ra0, ra1;
     // The prologue issues its loads in the loop's own order (A, B of step 0, A, B of
     // step 1): the wait counts at the loop head are merged from both ways in, and a
@@ -396,12 +442,18 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // a quarter of the bytes at K = 2048.
     auto step_even = [&] __attribute__((always_inline)) (int k, auto exact) {
         const int k2 = min(k + 2, nk - 1);
-        sc = sn;
+        if constexpr (kChunkS) {
+            // a new chunk opens at this pair: the chunk loaded two steps ago
+            if (((k >> 1) % PPC) == 0)
+                sc = sn;
+        } else {
+            sc = sn;
+        }
         if constexpr (PA == 2)
             load_a(ra0, cur, k2);
         else
             load_a(ra1, cur, min(k + 1, nk - 1));
-        compute(b0, 0, sc, 0, exact);
+        compute(b0, 0, sc, k >> 1, 0, exact);
         __builtin_amdgcn_sched_barrier(0);
         load_b(b0, cur, k2);
         load_s(sn, cur, k2);
@@ -415,7 +467,7 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             load_a(ra1, cur, k3);
         else
             load_a(ra0, cur, min(k + 2, nk - 1));
-        compute(b1, 1, sc, 1, exact);
+        compute(b1, 1, sc, k >> 1, 1, exact);
         __builtin_amdgcn_sched_barrier(0);
         load_b(b1, cur, k3);
         store_a(ra0, 0);
