@@ -121,8 +121,8 @@ __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
     // scales in 64-byte chunks (GScaleC) where the registers allow
     // (not the MXFP4 down kernel of the 16-row class: it would pass 128 VGPRs)
-    constexpr bool kChunkS =
-        MVLLM_CHUNK_S && !UNI && (MT == 4 || (MT == 1 && (DUAL || FMT == 4)));
+    constexpr bool kChunkS = MVLLM_CHUNK_S && !UNI && TERMS == 1 &&
+                             (MT == 4 || (MT == 1 && (DUAL || FMT == 4)));
     constexpr int PPC = gscale_ppc<FMT>();
     using Scl = std::conditional_t<kChunkS, GScaleC, GScale<FMT>>;
     constexpr int BM = 16 * MT;
