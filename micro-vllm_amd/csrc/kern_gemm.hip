@@ -56,6 +56,9 @@ struct GemmArgs {
 #ifndef MVLLM_CHUNK_S
 #define MVLLM_CHUNK_S 1
 #endif
+#ifndef MVLLM_DMA_A
+#define MVLLM_DMA_A 1
+#endif
 #ifndef MVLLM_PIPE_A
 #define MVLLM_PIPE_A 1
 #endif
@@ -127,8 +130,14 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     using Scl = std::conditional_t<kChunkS, GScaleC, GScale<FMT>>;
     constexpr int BM = 16 * MT;
     constexpr int PA = MT >= 8 ? 1 : 2;  // activation prefetch distance in K steps
-    constexpr int PL = BM * kGemmPitch;                  // bytes per plane per stage
-    constexpr int STAGE = gemm_stage_bytes(FMT, TERMS, MT);
+    // The one-term 128-row class loads its A tiles straight into LDS (buffer_load ... lds):
+    // no staging registers.  Its rows are then 512 bytes apart without padding, and a
+    // row's 16-byte chunks are XOR-swizzled by the row's low four bits, which keeps the
+    // fragment reads free of bank conflicts.
+    constexpr bool kDmaA = MVLLM_DMA_A && MT == 8 && TERMS == 1 && !UNI;
+    constexpr int APITCH = kDmaA ? kGemmBK * 2 : kGemmPitch;  // LDS bytes per A row
+    constexpr int PL = BM * APITCH;                  // bytes per plane per stage
+    constexpr int STAGE = kDmaA ? TERMS * PL : gemm_stage_bytes(FMT, TERMS, MT);
     constexpr int ACH = TERMS * BM * (kGemmBK / 8) / kGemmThreads;  // 16-byte chunks/thread
     // Row tiles' A fragments read one tile ahead where registers allow (the one-workgroup
     // classes: their MFMAs otherwise wait out each tile's LDS latency)
@@ -244,6 +253,29 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         }
     };
 
+    // kDmaA: the A tile of step k into LDS buffer buf.  DMA load i of wave w fills LDS rows
+    // 16 w + 2 i and + 1 (lane l: row + l / 32, physical chunk l % 32, which holds logical
+    // chunk (l % 32) ^ (row % 16)).  The item's rows are one buffer resource: rows past
+    // nrow lie beyond it and load as zeros (their results are never stored).
+    auto dma_a = [&] __attribute__((always_inline)) (const TaskD<FMT> &d, int k, int buf) {
+        if constexpr (kDmaA) {
+            const __amdgpu_buffer_rsrc_t ra =
+                buf_rsrc(A.pin + (size_t)d.jbase * (size_t)K, (uint32_t)d.nrow * (uint32_t)K * 2u);
+            const int dr = lane >> 5, pc = lane & 31;
+#pragma unroll
+            for (int i = 0; i < BM * APITCH / 1024 / 8; ++i) {
+                const int r = 16 * wave + 2 * i + dr;
+                const int lc = pc ^ ((2 * i + dr) & 15);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    ra,
+                    (__attribute__((address_space(3))) void *)(smem + buf * STAGE +
+                                                              (8 * wave + i) * 1024),
+                    16, (uint32_t)r * (uint32_t)K * 2u + 16u * (uint32_t)lc,
+                    (uint32_t)k * (uint32_t)(kGemmBK * 2), 0, 0);
+            }
+        }
+    };
+
     f4v acc[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -313,12 +345,15 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             }
             // A fragments of row tile mt (two 32-wide halves of group g, per term)
             auto read_a = [&] __attribute__((always_inline)) (int mt, bf16x8 (&a)[TERMS][2]) {
-                const char *ap = base + (mt * 16 + t) * kGemmPitch + (64 * g + 16 * q) * 2;
+                const char *rp = base + (mt * 16 + t) * APITCH;
 #pragma unroll
                 for (int tm = 0; tm < TERMS; ++tm)
 #pragma unroll
-                    for (int s = 0; s < 2; ++s)
-                        a[tm][s] = *reinterpret_cast<const bf16x8 *>(ap + tm * PL + 16 * s);
+                    for (int s = 0; s < 2; ++s) {
+                        const int off = kDmaA ? ((8 * g + 2 * q + s) ^ t) * 16
+                                              : (64 * g + 16 * q) * 2 + 16 * s;
+                        a[tm][s] = *reinterpret_cast<const bf16x8 *>(rp + tm * PL + off);
+                    }
             };
             bf16x8 an[TERMS][2];
             if constexpr (kPipeA)
@@ -425,7 +460,10 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // step 1): the wait counts at the loop head are merged from both ways in, and a
     // different order here would make the loop wait for step k + 1's weights too.
     auto prologue = [&] __attribute__((always_inline)) () {
-        load_a(ra0, cur, 0);
+        if constexpr (kDmaA)
+            dma_a(cur, 0, 0);
+        else
+            load_a(ra0, cur, 0);
         load_b(b0, cur, 0);
         load_s(sn, cur, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -433,7 +471,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             load_a(ra1, cur, min(1, nk - 1));
         load_b(b1, cur, min(1, nk - 1));
         __builtin_amdgcn_sched_barrier(0);
-        store_a(ra0, 0);
+        if constexpr (!kDmaA)
+            store_a(ra0, 0);
         __syncthreads();
     };
     // Even step k: LDS buffer 0, weights b0; stages A(k + 1) into buffer 1.  Prefetches
@@ -449,7 +488,9 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         } else {
             sc = sn;
         }
-        if constexpr (PA == 2)
+        if constexpr (kDmaA)
+            dma_a(cur, min(k + 1, nk - 1), 1);  // first: the barrier below waits for it only
+        else if constexpr (PA == 2)
             load_a(ra0, cur, k2);
         else
             load_a(ra1, cur, min(k + 1, nk - 1));
@@ -457,20 +498,24 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
         __builtin_amdgcn_sched_barrier(0);
         load_b(b0, cur, k2);
         load_s(sn, cur, k2);
-        store_a(ra1, 1);
+        if constexpr (!kDmaA)
+            store_a(ra1, 1);
         __syncthreads();
     };
     // odd step k + 1: LDS buffer 1, weights b1; stages A(k + 2) into buffer 0
     auto step_odd = [&] __attribute__((always_inline)) (int k, auto exact) {
         const int k3 = min(k + 3, nk - 1);
-        if constexpr (PA == 2)
+        if constexpr (kDmaA)
+            dma_a(cur, min(k + 2, nk - 1), 0);
+        else if constexpr (PA == 2)
             load_a(ra1, cur, k3);
         else
             load_a(ra0, cur, min(k + 2, nk - 1));
         compute(b1, 1, sc, k >> 1, 1, exact);
         __builtin_amdgcn_sched_barrier(0);
         load_b(b1, cur, k3);
-        store_a(ra0, 0);
+        if constexpr (!kDmaA)
+            store_a(ra0, 0);
         __syncthreads();
     };
     // The pair loop has no exit between its two steps: an exit there, merged by the
