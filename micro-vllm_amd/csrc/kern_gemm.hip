@@ -59,6 +59,9 @@ struct GemmArgs {
 #ifndef MVLLM_DMA_A
 #define MVLLM_DMA_A 1
 #endif
+#ifndef MVLLM_PIPE_B
+#define MVLLM_PIPE_B 1
+#endif
 #ifndef MVLLM_PIPE_A
 #define MVLLM_PIPE_A 1
 #endif
@@ -142,6 +145,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // Row tiles' A fragments read one tile ahead where registers allow (the one-workgroup
     // classes: their MFMAs otherwise wait out each tile's LDS latency)
     constexpr bool kPipeA = MVLLM_PIPE_A && MT >= 4 && TERMS == 1;
+    // the next group's weight shuffles ahead of this group's MFMAs (same classes)
+    constexpr bool kPipeB = MVLLM_PIPE_B && MT >= 4 && TERMS == 1;
     static_assert(ACH * kGemmThreads == TERMS * BM * (kGemmBK / 8), "A staging split");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -284,7 +289,7 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
 
 
     // step j (0 or 1) of pair p, whose scales are in sc
-    auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf,
+    auto compute1 = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf,
                                                          const Scl &sc, int p, int j, auto exact) {
         constexpr bool EXACT = decltype(exact)::value;
         const char *base = smem + buf * STAGE;
@@ -410,6 +415,171 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
                 // (register pressure)
                 __builtin_amdgcn_sched_barrier(0);
             }
+        }
+    };
+
+    // One group g (64 K) of step j of pair p: the operand shuffles of the two weight tiles
+    // and their scale words (LDS crossbar), the decode (VALU), then the MFMAs of every
+    // row tile.
+    struct GRaw {
+        uint32_t wx[2], wy[2], sw[2];
+    };
+    struct GDec {
+        bf16x8 bf[2][2];
+        float sg[2];
+        bool spec[2];  // EXACT int4: this lane's column scale is not finite
+    };
+    auto shuffle = [&] __attribute__((always_inline)) (const GStep<FMT> &b, const Scl &sc, int p,
+                                                         int j, int g, GRaw &r) {
+        // scale words of step j, groups 0-1 / 2-3, sit in lanes 4 t + 2 j and 4 t + 2 j + 1;
+        // chunked: MXFP4 pair p in lane 4 t + p % 4 (word 2 j + g / 2), int4 groups of step
+        // j in lane 4 t + 2 (p % 2) + j (component g)
+        const int ssrc = kChunkS ? (FMT == 7 ? 4 * (4 * t + p % PPC) : 4 * (4 * t + 2 * (p % PPC) + j))
+                                 : 4 * (4 * t + 2 * j);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            r.wx[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].x);
+            r.wy[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(src4, (int)b.w[m][g].y);
+            if constexpr (kChunkS && FMT == 4)
+                r.sw[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc, (int)sc.c[m][g]);
+            else if constexpr (kChunkS)
+                r.sw[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc, (int)sc.c[m][2 * j + (g >> 1)]);
+            else if constexpr (FMT == 4)
+                r.sw[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(
+                    ssrc + 4 * (g >> 1), (int)((g & 1) ? sc.s4[m].y : sc.s4[m].x));
+            else
+                r.sw[m] = (uint32_t)__builtin_amdgcn_ds_bpermute(ssrc + 4 * (g >> 1), (int)sc.s7[m]);
+        }
+    };
+    auto decode = [&] __attribute__((always_inline)) (const GRaw &r, int g, GDec &d, auto exact) {
+        constexpr bool EXACT = decltype(exact)::value;
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            d.spec[m] = false;
+            if constexpr (FMT == 4) {
+                d.sg[m] = __uint_as_float(r.sw[m]);
+            } else {  // lanes q < 2 take 32-block 2 g, q >= 2 block 2 g + 1
+                const int byte = 2 * (g & 1) + (q >> 1);
+                d.sg[m] = __uint_as_float(((r.sw[m] >> (8 * byte)) & 0xffu) << 23);
+            }
+            if constexpr (FMT == 7 && EXACT) {
+                d.bf[m][0] = decode_b7_exact(r.wx[m], d.sg[m]);
+                d.bf[m][1] = decode_b7_exact(r.wy[m], d.sg[m]);
+            } else if constexpr (FMT == 4) {
+                d.bf[m][0] = decode_b4_signed(r.wx[m]);
+                d.bf[m][1] = decode_b4_signed(r.wy[m]);
+                if constexpr (EXACT) {
+                    // the reference's x * ((n - 8) * scale): a non-finite scale enters each
+                    // product, which then takes the high term of x alone (its low terms
+                    // would turn inf * 0 into NaN)
+                    d.spec[m] = nonfinite(d.sg[m]);
+                    if (d.spec[m]) {
+                        d.bf[m][0] = mul_bf16x8_exact(d.bf[m][0], d.sg[m]);
+                        d.bf[m][1] = mul_bf16x8_exact(d.bf[m][1], d.sg[m]);
+                    }
+                } else {
+                    exc |= (uint32_t)nonfinite(d.sg[m]);
+                }
+            } else {
+                d.bf[m][0] = decode_b<FMT>(r.wx[m], d.sg[m]);
+                d.bf[m][1] = decode_b<FMT>(r.wy[m], d.sg[m]);
+                exc |= (uint32_t)b7_exceptional(d.sg[m]);
+            }
+        }
+    };
+    auto mfmas = [&] __attribute__((always_inline)) (const char *base, int g, const GDec &d,
+                                                       auto exact) {
+        constexpr bool EXACT = decltype(exact)::value;
+        // A fragments of row tile mt (two 32-wide halves of group g, per term)
+        auto read_a = [&] __attribute__((always_inline)) (int mt, bf16x8 (&a)[TERMS][2]) {
+            const char *rp = base + (mt * 16 + t) * APITCH;
+#pragma unroll
+            for (int tm = 0; tm < TERMS; ++tm)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int off = kDmaA ? ((8 * g + 2 * q + s) ^ t) * 16
+                                          : (64 * g + 16 * q) * 2 + 16 * s;
+                    a[tm][s] = *reinterpret_cast<const bf16x8 *>(rp + tm * PL + off);
+                }
+        };
+        bf16x8 an[TERMS][2];
+        if constexpr (kPipeA)
+            read_a(0, an);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            bf16x8 a[TERMS][2];
+            if constexpr (kPipeA) {
+                // the next row tile's fragments are read before this tile's MFMAs, so
+                // their LDS latency runs under the MFMAs
+#pragma unroll
+                for (int tm = 0; tm < TERMS; ++tm)
+                    a[tm][0] = an[tm][0], a[tm][1] = an[tm][1];
+                if (mt + 1 < MT)
+                    read_a(mt + 1, an);
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                read_a(mt, a);
+            }
+            if constexpr (FMT == 4) {
+                // each 64-wide group is its own chain over n - 8, then one f32 FMA applies
+                // the group's scale
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    f4v c = f4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; ++tm) {
+                        bf16x8 b0 = d.bf[m][0], b1 = d.bf[m][1];
+                        if (EXACT && tm > 0 && d.spec[m])
+                            b0 = b1 = bf16x8{};
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], b0, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], b1, c, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[mt][m][i] = EXACT && d.spec[m] ? acc[mt][m][i] + c[i]
+                                                           : fmaf(d.sg[m], c[i], acc[mt][m][i]);
+                    // keep the scaling here: sunk below the next step's loads, it drags a
+                    // wait for those loads in with it
+                    asm volatile("" : "+v"(acc[mt][m]));
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+#pragma unroll
+                    for (int tm = 0; tm < TERMS; ++tm) {
+                        acc[mt][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][0], d.bf[m][0],
+                                                                             acc[mt][m], 0, 0, 0);
+                        acc[mt][m] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[tm][1], d.bf[m][1],
+                                                                             acc[mt][m], 0, 0, 0);
+                    }
+            }
+            // one row tile's A fragments live at a time, or two with kPipeA (register
+            // pressure)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // step j (0 or 1) of pair p, whose scales are in sc.  kPipeB: group g + 1's operand
+    // shuffles are issued before group g's MFMAs and decoded after them, so the shuffles'
+    // LDS latency runs under the MFMAs instead of ahead of every group.
+    auto compute = [&] __attribute__((always_inline)) (const GStep<FMT> &b, int buf,
+                                                         const Scl &sc, int p, int j, auto exact) {
+        const char *base = smem + buf * STAGE;
+        if constexpr (kPipeB) {
+            GRaw r;
+            GDec d;
+            shuffle(b, sc, p, j, 0, r);
+            decode(r, 0, d, exact);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                if (g < 3)
+                    shuffle(b, sc, p, j, g + 1, r);
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(base, g, d, exact);
+                if (g < 3)
+                    decode(r, g + 1, d, exact);
+            }
+        } else {
+            compute1(b, buf, sc, p, j, exact);
         }
     };
 
