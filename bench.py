@@ -388,26 +388,24 @@ def route_timing(torch, mvllm_hip, T, E, k, reps=100):
 
 
 def cpu_route_baseline(np, scores, k, budget_s=2.0):
-    """The host routing on the same scores: moe_topk per token (oracle/_ref build when
-    present, else the C restatement) and the segments (C restatement), one thread."""
+    """The host routing on the same scores, one thread: moe_topk for every token in one
+    native call (oracle/_ref build when present, else the C restatement), then the
+    segments (C restatement), so the figure carries two ctypes calls, not one per token."""
     import oracle
     kind = "reference" if oracle.have_ref() else "port"
     topk = oracle.CpuMoe("ref" if kind == "reference" else "oracle")
     seg = oracle.CpuMoe("oracle")
     choice, mix = scores
     T, E = choice.shape
-    idx, wt = np.empty((T, k), np.int32), np.empty((T, k), np.float32)
     calls, t0 = 0, time.perf_counter()
     while True:
-        for t in range(T):
-            _, idx[t], wt[t] = topk.moe_topk(choice[t], k, mix[t])
+        _, idx, wt = topk.moe_topk_batch(choice, k, mix)
         seg.moe_segments(idx, wt, T, k, E)
         calls += 1
         if time.perf_counter() - t0 > budget_s:
             break
     return round((time.perf_counter() - t0) / calls * 1e6, 1), \
-        f"{kind}; Python-driven: one ctypes call per token (~1 us of call overhead each), " \
-        "then the segments"
+        f"{kind}; moe_topk over all tokens in one native call, then the segments"
 
 
 def staged(args, np, torch, mvllm_hip, synth, cfg, T, steps, warmup, miss_rate, cpu_seconds):

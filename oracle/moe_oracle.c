@@ -298,6 +298,18 @@ int orc_moe_topk(const float *choice, int n, int k, int *idx, float *w, const fl
     return k;
 }
 
+/* moe_topk over n_tok tokens in one call (choice/mix rows of n floats, idx/w rows of k):
+ * the per-token loop of the reference's prefill router, so a host timing of it carries
+ * no per-token call overhead.  Returns the per-token k. */
+int orc_moe_topk_batch(const float *choice, int n_tok, int n, int k, int *idx, float *w,
+                       const float *mix) {
+    int kk = 0;
+    for (int t = 0; t < n_tok; ++t)
+        kk = orc_moe_topk(choice + (size_t)t * n, n, k, idx + (size_t)t * k, w + (size_t)t * k,
+                          mix ? mix + (size_t)t * n : NULL);
+    return kk;
+}
+
 static int cmp_int(const void *a, const void *b) {
     const int x = *(const int *)a, y = *(const int *)b;
     return (x > y) - (x < y);

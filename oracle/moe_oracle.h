@@ -67,6 +67,8 @@ int orc_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void *const
  * src/model/ops.cpp:1082-1099 (moe_union_ids), src/model/glm53.cpp:1938-1971
  * (per-expert gather loop). */
 int orc_moe_topk(const float *choice, int n, int k, int *idx, float *w, const float *mix);
+int orc_moe_topk_batch(const float *choice, int n_tok, int n, int k, int *idx, float *w,
+                       const float *mix);
 int orc_moe_union_ids(const int *idx, int n_tok, int topk, int *out, int out_cap);
 /* Segments for one batched moe_block call that reproduces moe_layer_n's
  * per-expert loop: eids[nb] (ascending), xoff/nr[nb], and per routed row j:

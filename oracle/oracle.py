@@ -68,6 +68,7 @@ class CpuMoe:
             "mx4_scale": (_f, [C.c_uint8]),
             "moe_topk": (_i, [_p, _i, _i, _p, _p, _p]),
             "moe_union_ids": (_i, [_p, _i, _i, _p, _i]),
+            "moe_topk_batch": (_i, [_p, _i, _i, _i, _p, _p, _p]),
             "bf16_round": (_f, [_f]),
             "e8m0_decode": (_f, [C.c_uint8]),
             "e2m1_decode": (_f, [C.c_uint8]),
@@ -213,6 +214,16 @@ class CpuMoe:
         kk = self.fn("moe_topk")(_ptr(choice), n, k, _ptr(idx), _ptr(w),
                                  _ptr(None if mix is None else np.ascontiguousarray(mix, np.float32)))
         return kk, idx[:max(kk, 0)], w[:max(kk, 0)]
+
+    def moe_topk_batch(self, choice, k, mix=None):
+        """moe_topk over every row of choice [T, n] in one native call."""
+        choice = np.ascontiguousarray(choice, np.float32)
+        T, n = choice.shape
+        idx = np.full((T, max(k, 1)), -7, np.int32)
+        w = np.zeros((T, max(k, 1)), np.float32)
+        kk = self.fn("moe_topk_batch")(_ptr(choice), T, n, k, _ptr(idx), _ptr(w),
+                                       _ptr(None if mix is None else np.ascontiguousarray(mix, np.float32)))
+        return kk, idx[:, :max(kk, 0)], w[:, :max(kk, 0)]
 
     def moe_union_ids(self, idx, n_tok, topk, cap):
         idx = np.ascontiguousarray(idx, np.int32)

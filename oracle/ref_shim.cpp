@@ -54,6 +54,15 @@ void ref_silu_mul(float *g, const float *u, int n) { quant::silu_mul(g, u, n); }
 int ref_moe_topk(const float *choice, int n, int k, int *idx, float *w, const float *mix) {
     return moe_topk(choice, n, k, idx, w, mix);
 }
+// The reference's moe_topk for n_tok tokens in one call (rows of n scores, rows of k out).
+int ref_moe_topk_batch(const float *choice, int n_tok, int n, int k, int *idx, float *w,
+                       const float *mix) {
+    int kk = 0;
+    for (int t = 0; t < n_tok; ++t)
+        kk = moe_topk(choice + (size_t)t * n, n, k, idx + (size_t)t * k, w + (size_t)t * k,
+                      mix ? mix + (size_t)t * n : nullptr);
+    return kk;
+}
 int ref_moe_union_ids(const int *idx, int n_tok, int topk, int *out, int cap) {
     return moe_union_ids(idx, n_tok, topk, out, cap);
 }

@@ -223,6 +223,22 @@ def test_topk_brute_force(orc):
         assert np.array_equal(w, exp.astype(np.float32))
 
 
+def test_topk_batch_matches_per_token(orc):
+    """The one-call batch (timed by bench.py's routing baseline) gives each token's
+    moe_topk, in both libraries."""
+    rng = np.random.default_rng(6)
+    T, n, k = 19, 33, 5
+    choice = rng.integers(-3, 4, size=(T, n)).astype(np.float32)
+    mix = rng.uniform(-0.2, 1.0, size=(T, n)).astype(np.float32)
+    import oracle
+    for lib in [orc] + ([oracle.CpuMoe("ref")] if oracle.have_ref() else []):
+        kk, idx, w = lib.moe_topk_batch(choice, k, mix)
+        assert kk == k
+        for t in range(T):
+            _, i1, w1 = orc.moe_topk(choice[t], k, mix[t])
+            assert np.array_equal(idx[t], i1) and np.array_equal(_bits(w[t]), _bits(w1))
+
+
 def test_segments_invariants(orc):
     rng = np.random.default_rng(9)
     T, E, k = 37, 12, 4
