@@ -453,6 +453,9 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
 #pragma unroll
         for (int n = 0; n < NT; ++n)
             load_scales<FMT>(sc[n], rs[n], vs[n]);
+        // the scales ahead of the weight blocks: the check before the loop waits for the
+        // scales only, so no wave drains its weight prefetch before the loop starts
+        asm volatile("" ::: "memory");
 #pragma unroll
         for (int u = 0; u < NU; ++u)
 #pragma unroll
