@@ -53,18 +53,6 @@ struct GemmArgs {
     float act_a, act_b;
 };
 
-#ifndef MVLLM_CHUNK_S
-#define MVLLM_CHUNK_S 1
-#endif
-#ifndef MVLLM_DMA_A
-#define MVLLM_DMA_A 1
-#endif
-#ifndef MVLLM_PIPE_B
-#define MVLLM_PIPE_B 1
-#endif
-#ifndef MVLLM_PIPE_A
-#define MVLLM_PIPE_A 1
-#endif
 constexpr int kGemmThreads = 512;
 constexpr int kGemmBK = 256;
 constexpr int kGemmPitch = kGemmBK * 2 + 16;  // LDS bytes per A row and plane (+16: banks)
@@ -127,7 +115,7 @@ __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
     // scales in 64-byte chunks (GScaleC) where the registers allow
     // (not the MXFP4 down kernel of the 16-row class: it would pass 128 VGPRs)
-    constexpr bool kChunkS = MVLLM_CHUNK_S && !UNI && TERMS == 1 &&
+    constexpr bool kChunkS = !UNI && TERMS == 1 &&
                              (MT == 4 || (MT == 1 && (DUAL || FMT == 4)));
     constexpr int PPC = gscale_ppc<FMT>();
     using Scl = std::conditional_t<kChunkS, GScaleC, GScale<FMT>>;
@@ -137,16 +125,16 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     // no staging registers.  Its rows are then 512 bytes apart without padding, and a
     // row's 16-byte chunks are XOR-swizzled by the row's low four bits, which keeps the
     // fragment reads free of bank conflicts.
-    constexpr bool kDmaA = MVLLM_DMA_A && MT == 8 && TERMS == 1 && !UNI;
+    constexpr bool kDmaA = MT == 8 && TERMS == 1 && !UNI;
     constexpr int APITCH = kDmaA ? kGemmBK * 2 : kGemmPitch;  // LDS bytes per A row
     constexpr int PL = BM * APITCH;                  // bytes per plane per stage
     constexpr int STAGE = kDmaA ? TERMS * PL : gemm_stage_bytes(FMT, TERMS, MT);
     constexpr int ACH = TERMS * BM * (kGemmBK / 8) / kGemmThreads;  // 16-byte chunks/thread
     // Row tiles' A fragments read one tile ahead where registers allow (the one-workgroup
     // classes: their MFMAs otherwise wait out each tile's LDS latency)
-    constexpr bool kPipeA = MVLLM_PIPE_A && MT >= 4 && TERMS == 1;
+    constexpr bool kPipeA = MT >= 4 && TERMS == 1;
     // the next group's weight shuffles ahead of this group's MFMAs (same classes)
-    constexpr bool kPipeB = MVLLM_PIPE_B && MT >= 4 && TERMS == 1;
+    constexpr bool kPipeB = MT >= 4 && TERMS == 1;
     static_assert(ACH * kGemmThreads == TERMS * BM * (kGemmBK / 8), "A staging split");
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
