@@ -16,6 +16,7 @@ Prints ONE JSON line on stdout; details go to stderr.
                   [--fp4act] [--no-extra] [--no-cpu]
 """
 import argparse
+import contextlib
 import json
 import os
 import sys
@@ -397,14 +398,16 @@ def cpu_route_baseline(np, scores, k, budget_s=2.0):
     seg = oracle.CpuMoe("oracle")
     choice, mix = scores
     T, E = choice.shape
-    calls, t0 = 0, time.perf_counter()
-    while True:
-        _, idx, wt = topk.moe_topk_batch(choice, k, mix)
-        seg.moe_segments(idx, wt, T, k, E)
-        calls += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    return round((time.perf_counter() - t0) / calls * 1e6, 1), \
+    with one_core():
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            _, idx, wt = topk.moe_topk_batch(choice, k, mix)
+            seg.moe_segments(idx, wt, T, k, E)
+            calls += 1
+            if time.perf_counter() - t0 > budget_s:
+                break
+        t_call = (time.perf_counter() - t0) / calls
+    return round(t_call * 1e6, 1), \
         f"{kind}; moe_topk over all tokens in one native call, then the segments"
 
 
@@ -635,6 +638,35 @@ def layer_pipeline(np, torch, mvllm_hip, synth, cfg, n_layers=12, steps=4, miss_
             "value": round(1e6 / (t_pipe * n_layers), 3), "unit": "tokens/s (12 layers)"}
 
 
+def cpu_model():
+    """The host CPU's model name (reported beside the host baselines)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+@contextlib.contextmanager
+def one_core():
+    """Pin the process to one of its CPUs while a single-threaded host baseline is timed
+    (the reference's host path is single-threaded); yields that CPU's index or None."""
+    try:
+        old = os.sched_getaffinity(0)
+        cpu = min(old)
+        os.sched_setaffinity(0, {cpu})
+    except (AttributeError, OSError):
+        old, cpu = None, None
+    try:
+        yield cpu
+    finally:
+        if old is not None:
+            os.sched_setaffinity(0, old)
+
+
 def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):
     """The reference's host moe_block (oracle/_ref build when present, else the C
     restatement) on layer 0's experts, single thread, bounded to ~budget_s.  Decode
@@ -652,6 +684,17 @@ def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):
     def expert(i):
         return synth.blob_pieces(pool[i].cpu().numpy(), fmt, D, I, off)
 
+    with one_core() as pinned:
+        per, sample = _cpu_time(np, cpu, w, expert, macs_e, macs_total, fmt, D, I, T,
+                                budget_s)
+    log(f"cpu baseline ({kind}, 1 thread): {per*1e3:.1f} ms/call ({sample})")
+    return {"value": round(T / per, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
+            "sample": sample, "ms_per_call": round(per * 1e3, 3), "nproc": os.cpu_count(),
+            "pinned_cpu": pinned, "cpu_model": cpu_model()}
+
+
+def _cpu_time(np, cpu, w, expert, macs_e, macs_total, fmt, D, I, T, budget_s):
+    """Seconds per moe_block call of the host baseline and a description of the sample."""
     if macs_total / 1e9 <= 4 * budget_s:  # whole calls (about 1 GMAC/s on one core)
         ex = [expert(i) for i in range(w.nb)]
         lists = [[e[k] for e in ex] for k in range(6)]
@@ -685,9 +728,7 @@ def cpu_baseline(np, torch, w, pool, stride, off, fmt, D, I, T, budget_s):
         per = el * macs_total / done
         sample = (f"{n_e} of {w.nb} experts ({int(done / (3 * D * I))} of {int(w.nr.sum())} rows) "
                   f"run as nb=1 calls in {el:.1f} s; the full call extrapolated by MACs")
-    log(f"cpu baseline ({kind}, 1 thread): {per*1e3:.1f} ms/call ({sample})")
-    return {"value": round(T / per, 3), "unit": "tokens/s", "cores": 1, "kind": kind,
-            "sample": sample, "ms_per_call": round(per * 1e3, 3), "nproc": os.cpu_count()}
+    return per, sample
 
 
 if __name__ == "__main__":
