@@ -42,7 +42,8 @@ struct GemmArgs {
     int nrows_all;
     const __bf16 *pin;  // A planes [TERMS][rcap][K] (int4: 8-blocks in slot order)
     __bf16 *pout;       // dual: H planes [TERMS][rcap][O]
-    float *out;         // single: Y [rcap][O] f32
+    float *out;         // single: Y [rcap][O] f32; dual: H [rcap][O] f32 instead of planes
+                        // when set (the native-MXFP4 call quantizes H afterwards)
     int nbn;            // column blocks per item
     int n_tasks;        // items * nbn
     const int *n_items_dev;  // non-null: the item count is in device memory (a grid sized
@@ -586,9 +587,13 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
                     const int col = d.col0 + t;
                     const int pos = (col & ~7) + a_slot<FMT>(col & 7);
                     if (r < d.nrow) {
+                        if (A.out) {
+                            A.out[(size_t)j * O + col] = h;
+                        } else {
 #pragma unroll
-                        for (int tm = 0; tm < TERMS; ++tm)
-                            A.pout[((size_t)tm * rcap + j) * O + pos] = tt[tm];
+                            for (int tm = 0; tm < TERMS; ++tm)
+                                A.pout[((size_t)tm * rcap + j) * O + pos] = tt[tm];
+                        }
                     }
                 } else {
                     if (r < d.nrow) {

@@ -95,9 +95,19 @@ __device__ __forceinline__ int ceil_log2_normal(float v) {
 // launcher refuses more than 2^31 blocks.
 constexpr int kQU = 4;
 
+// e2m1 code -> value (0, 0.5, 1, 1.5, 2, 3, 4, 6; bit 3 the sign)
+__device__ __forceinline__ float e2m1_value(uint32_t c) {
+    const uint32_t m = c & 7u;
+    const float v = m < 4u ? 0.5f * (float)m : (float)(2u << ((m - 4u) >> 1)) * (1.f + 0.5f * (float)(m & 1u));
+    return (c & 8u) ? -v : v;
+}
+
+// planes (nullable): also the quantized values themselves as bf16 rows [n][K] (code value
+// x 2^ex has at most two significant bits, so the bf16 holds it exactly; it is the f32
+// value's upper half).
 __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const int *rows_map,
                                                         int n, int K, uint8_t *codes,
-                                                        uint8_t *scales) {
+                                                        uint8_t *scales, __bf16 *planes) {
     const uint32_t nb = (uint32_t)(K / 32);
     const uint32_t total = (uint32_t)n * nb;  // blocks
     const uint32_t lane = threadIdx.x & 63, e8 = lane & 7;
@@ -150,13 +160,24 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
                                               blk[u] * 16 + 2 * e8) = (uint16_t)packed;
                 if (e8 == 0)
                     scales[bid] = (uint8_t)(ex + 127);
+                if (planes) {
+                    uint32_t h[2];
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const float lo = ldexpf(e2m1_value((packed >> (8 * i)) & 15u), ex);
+                        const float hi = ldexpf(e2m1_value((packed >> (8 * i + 4)) & 15u), ex);
+                        h[i] = (__float_as_uint(lo) >> 16) | (__float_as_uint(hi) & 0xffff0000u);
+                    }
+                    *reinterpret_cast<uint2 *>(planes + (size_t)row[u] * (size_t)K +
+                                               blk[u] * 32 + 4 * e8) = make_uint2(h[0], h[1]);
+                }
             }
         }
     }
 }
 
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
-                                 hipStream_t st, const int *rows_map) {
+                                 hipStream_t st, const int *rows_map, void *planes) {
     if (n <= 0 || K <= 0 || K % 32 || (size_t)n * (K / 32) >= (size_t(1) << 31) ||
         (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
@@ -164,7 +185,7 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
     const size_t wgs = (waves + 3) / 4;
     const unsigned grid = (unsigned)(wgs < 4096 ? wgs : 4096);
     hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid), dim3(256), 0, st, x, rows_map, n, K, codes,
-                       scales);
+                       scales, static_cast<__bf16 *>(planes));
     return hipGetLastError();
 }
 

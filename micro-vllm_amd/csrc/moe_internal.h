@@ -56,9 +56,11 @@ hipError_t launch_dequant_bf16path(int fmt, const void *packed, const void *scal
                                    int K, float *w, hipStream_t st);
 hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, int row16,
                            hipStream_t st);
-// MXFP4 activation quantization of n rows of K (row j = x row rows_map[j], or j).
+// MXFP4 activation quantization of n rows of K (row j = x row rows_map[j], or j); planes
+// (optional, 8-byte aligned): the quantized values as bf16 rows [n][K] as well.
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
-                                 hipStream_t st, const int *rows_map = nullptr);
+                                 hipStream_t st, const int *rows_map = nullptr,
+                                 void *planes = nullptr);
 
 // Routing on the device (kern_route.hip): moe_topk per token, and the segments of one
 // batched moe_block call.  Bit-exact with the host versions.
@@ -155,6 +157,7 @@ size_t gemm_lds_bytes(int fmt, int terms, int mt);
 // range of tasks (an item's column blocks share one L2), 0 = task = workgroup index.
 void gemm_set_xcd(bool on);
 bool gemm_xcd();
+// dual with out set: H is written to out as f32 rows [rcap][O] instead of planes to pout.
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,
                        int K, int O, int rcap, int act, float act_a, float act_b,
@@ -193,6 +196,11 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int rows, in
 // Requires K % 256 == 0, O % 128 (dual) / % 256 (single) == 0, 16-byte aligned weights,
 // 8-byte aligned scales.
 constexpr int kFp4MaxMt = 4;
+// Row classes of a native-MXFP4 call (option fp4act) up to this one take the bf16 grouped
+// GEMM on bf16 copies of the quantized activations instead (launch_quantize_mxfp4's
+// planes): the same exact products, streamed faster (c4: gate/up 16-row class 794 ->
+// ~680 us, 32-row 347 -> ~270 us).
+constexpr int kFp4BfMaxMt = 2;
 size_t fp4_lds_bytes(int mt);
 hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *items,
                            int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,

@@ -596,6 +596,7 @@ void buf_sizes(const CallCfg &cc, size_t R, int D, int I, size_t sz[5]) {
         sz[0] = R * I * 4;
         sz[1] = R * D * 4;
         sz[2] = R * (I / 2 + I / 32);
+        sz[3] = R * (D + I) * 2;  // bf16 planes of the quantized x and H (kFp4BfMaxMt)
         sz[4] = R * (D / 2 + D / 32);
     } else if (cc.gemm) {
         sz[1] = R * D * 4;
@@ -884,11 +885,19 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
     HIP_TRY(mark(0));
     if (cc.fp4) {
         // activations quantized to MXFP4 (bit-exact with fp4_activation_qdq), the gate/up
-        // GEMM writes H f32, H is quantized, the down GEMM writes Y
+        // GEMM writes H f32, H is quantized, the down GEMM writes Y.  The 16- and 32-row
+        // classes run the bf16 grouped GEMM on the quantized values as bf16 planes (exact
+        // copies of them, written by the quantizer): it streams those classes' weights
+        // faster than the scaled-FP4 kernel, with the same exact products.
         uint8_t *xq = static_cast<uint8_t *>(B.Xp), *xsc = xq + R * (D / 2);
         uint8_t *hq = static_cast<uint8_t *>(B.Ph), *hsc = hq + R * (I / 2);
         float *H = static_cast<float *>(B.H);
-        HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows));
+        bool bf = false;
+        for (int c = 0; c < cc.n_gcls; ++c)
+            bf = bf || cc.gcls[c].mt <= kFp4BfMaxMt;
+        __bf16 *xb = bf ? static_cast<__bf16 *>(B.HP) : nullptr;
+        __bf16 *hb = bf ? xb + R * (size_t)D : nullptr;
+        HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows, xb));
         HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             if (part == 1 && gate_event)
@@ -898,20 +907,31 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
                 const size_t i0 = part ? g.it_split : g.it0, i1 = part ? g.it1 : g.it_split;
                 if (i1 <= i0)
                     continue;
-                HIP_TRY(launch_gemm_fp4(true, g.mt, dp.ew, dp.items + 4 * i0,
-                                        static_cast<int>(i1 - i0), xq, xsc, H, nullptr, D, I,
-                                        rcap, act, a, b, st));
+                if (g.mt <= kFp4BfMaxMt)
+                    HIP_TRY(launch_gemm(fmt, true, 1, g.mt, dp.ew, dp.items + 4 * i0,
+                                        static_cast<int>(i1 - i0), xb, nullptr, H, D, I, rcap,
+                                        act, a, b, st));
+                else
+                    HIP_TRY(launch_gemm_fp4(true, g.mt, dp.ew, dp.items + 4 * i0,
+                                            static_cast<int>(i1 - i0), xq, xsc, H, nullptr, D,
+                                            I, rcap, act, a, b, st));
                 C.stats[13] += 1;
             }
         }
         HIP_TRY(mark(2));
-        HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st));
+        HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st, nullptr, hb));
         HIP_TRY(mark(3));
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
-            HIP_TRY(launch_gemm_fp4(false, g.mt, dp.ew, dp.items + 4 * g.it0,
-                                    static_cast<int>(g.it1 - g.it0), hq, hsc, nullptr,
+            if (g.mt <= kFp4BfMaxMt)
+                HIP_TRY(launch_gemm(fmt, false, 1, g.mt, dp.ew, dp.items + 4 * g.it0,
+                                    static_cast<int>(g.it1 - g.it0), hb, nullptr,
                                     static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f, st));
+            else
+                HIP_TRY(launch_gemm_fp4(false, g.mt, dp.ew, dp.items + 4 * g.it0,
+                                        static_cast<int>(g.it1 - g.it0), hq, hsc, nullptr,
+                                        static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f,
+                                        st));
             C.stats[14] += 1;
         }
     } else if (cc.f32) {
