@@ -104,10 +104,11 @@ __device__ __forceinline__ float e2m1_value(uint32_t c) {
 
 // planes (nullable): also the quantized values themselves as bf16 rows [n][K] (code value
 // x 2^ex has at most two significant bits, so the bf16 holds it exactly; it is the f32
-// value's upper half).
+// value's upper half), for the rows j with pmask[j] != 0 (all rows when pmask is null).
 __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const int *rows_map,
                                                         int n, int K, uint8_t *codes,
-                                                        uint8_t *scales, __bf16 *planes) {
+                                                        uint8_t *scales, __bf16 *planes,
+                                                        const uint8_t *pmask) {
     const uint32_t nb = (uint32_t)(K / 32);
     const uint32_t total = (uint32_t)n * nb;  // blocks
     const uint32_t lane = threadIdx.x & 63, e8 = lane & 7;
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
                                               blk[u] * 16 + 2 * e8) = (uint16_t)packed;
                 if (e8 == 0)
                     scales[bid] = (uint8_t)(ex + 127);
-                if (planes) {
+                if (planes && (!pmask || pmask[row[u]])) {
                     uint32_t h[2];
 #pragma unroll
                     for (int i = 0; i < 2; ++i) {
@@ -177,7 +178,8 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
 }
 
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
-                                 hipStream_t st, const int *rows_map, void *planes) {
+                                 hipStream_t st, const int *rows_map, void *planes,
+                                 const uint8_t *pmask) {
     if (n <= 0 || K <= 0 || K % 32 || (size_t)n * (K / 32) >= (size_t(1) << 31) ||
         (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
@@ -185,7 +187,7 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
     const size_t wgs = (waves + 3) / 4;
     const unsigned grid = (unsigned)(wgs < 4096 ? wgs : 4096);
     hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid), dim3(256), 0, st, x, rows_map, n, K, codes,
-                       scales, static_cast<__bf16 *>(planes));
+                       scales, static_cast<__bf16 *>(planes), pmask);
     return hipGetLastError();
 }
 

@@ -57,10 +57,11 @@ hipError_t launch_dequant_bf16path(int fmt, const void *packed, const void *scal
 hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, int row16,
                            hipStream_t st);
 // MXFP4 activation quantization of n rows of K (row j = x row rows_map[j], or j); planes
-// (optional, 8-byte aligned): the quantized values as bf16 rows [n][K] as well.
+// (optional, 8-byte aligned): the quantized values as bf16 rows [n][K] as well, for the
+// rows j with pmask[j] != 0 (every row when pmask is null).
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st, const int *rows_map = nullptr,
-                                 void *planes = nullptr);
+                                 void *planes = nullptr, const uint8_t *pmask = nullptr);
 
 // Routing on the device (kern_route.hip): moe_topk per token, and the segments of one
 // batched moe_block call.  Bit-exact with the host versions.

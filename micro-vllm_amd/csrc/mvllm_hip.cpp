@@ -639,6 +639,7 @@ struct DevPlan {
     float *ent_w, *rw;
     DecDesc *gu_desc, *dn_desc;  // decode kernels: one descriptor per item of each phase
     DecDesc *dn_desc_dev;        // dn_desc in device memory (a copy the gate/up kernel makes)
+    uint8_t *pmask;              // native FP4: 1 for the compact rows that get bf16 planes
     const DecDesc *gu_host;      // gu_desc's copy in the pinned slot (host memory)
     int slot;  // plan slot index
 };
@@ -732,7 +733,9 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     const size_t n_gu = cc.mfma ? cc.gu.it1 - cc.gu.it0 : 0;
     const size_t n_dn = cc.mfma ? cc.dn.it1 - cc.dn.it0 : 0;
     const size_t b_dg = n_gu * sizeof(DecDesc), b_dd = n_dn * sizeof(DecDesc);
-    const size_t total = b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw + b_dg + b_dd;
+    const size_t b_pm = cc.fp4 ? al(R) : 0;  // native FP4: rows with bf16 planes
+    const size_t total =
+        b_ew + b_x + b_tp + b_er + b_or + b_ew2 + b_it + b_rd + b_rw + b_dg + b_dd + b_pm;
     if (dev_dst) {
         if (total > s.host.cap || total > dev_cap) {
             set_err("plan of " + std::to_string(total) + " bytes exceeds the preallocated " +
@@ -788,6 +791,22 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
                    reinterpret_cast<DecDesc *>(h + o_dd));
     }
     o += b_dg + b_dd;
+    // native FP4: the compact rows of the classes that run the bf16 GEMM
+    const size_t o_pm = o;
+    if (b_pm) {
+        uint8_t *pm = reinterpret_cast<uint8_t *>(h + o_pm);
+        std::memset(pm, 0, R);
+        for (int c = 0; c < cc.n_gcls; ++c) {
+            const GemmCls &g = cc.gcls[c];
+            if (g.mt > kFp4BfMaxMt)
+                continue;
+            for (size_t i = g.it0; i < g.it1; ++i) {
+                const int *it = &cc.items[4 * i];
+                std::memset(pm + P.ew[it[0]].row0 + it[1], 1, (size_t)it[2]);
+            }
+        }
+        o += b_pm;
+    }
     // The decode kernels with the folded combine read nothing of the plan but their
     // descriptors, and those straight from this pinned slot (no copy, no copy launch):
     // the slot is rewritten only after the call that read it has finished (above).
@@ -810,6 +829,7 @@ int upload_plan(Ctx &C, const Plan &P, const CallCfg &cc, hipStream_t st, DevPla
     dp.gu_host = reinterpret_cast<const DecDesc *>(h + o_dg);
     dp.dn_desc = reinterpret_cast<DecDesc *>(d + o_dd);
     dp.dn_desc_dev = reinterpret_cast<DecDesc *>(dbase + o_dd);
+    dp.pmask = b_pm ? reinterpret_cast<uint8_t *>(d + o_pm) : nullptr;
     if (!zero_copy)
         dp.dn_desc_dev = dp.dn_desc;  // already there
     dp.slot = si;
@@ -897,7 +917,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
             bf = bf || cc.gcls[c].mt <= kFp4BfMaxMt;
         __bf16 *xb = bf ? static_cast<__bf16 *>(B.HP) : nullptr;
         __bf16 *hb = bf ? xb + R * (size_t)D : nullptr;
-        HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows, xb));
+        HIP_TRY(launch_quantize_mxfp4(in, rcap, D, xq, xsc, st, in_rows, xb, dp.pmask));
         HIP_TRY(mark(1));
         for (int part = 0; part < 2; ++part) {
             if (part == 1 && gate_event)
@@ -919,7 +939,7 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
             }
         }
         HIP_TRY(mark(2));
-        HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st, nullptr, hb));
+        HIP_TRY(launch_quantize_mxfp4(H, rcap, I, hq, hsc, st, nullptr, hb, dp.pmask));
         HIP_TRY(mark(3));
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
