@@ -596,7 +596,10 @@ void buf_sizes(const CallCfg &cc, size_t R, int D, int I, size_t sz[5]) {
         sz[0] = R * I * 4;
         sz[1] = R * D * 4;
         sz[2] = R * (I / 2 + I / 32);
-        sz[3] = R * (D + I) * 2;  // bf16 planes of the quantized x and H (kFp4BfMaxMt)
+        bool bf = false;  // bf16 planes of the quantized x and H (kFp4BfMaxMt)
+        for (int c = 0; c < cc.n_gcls; ++c)
+            bf = bf || cc.gcls[c].mt <= kFp4BfMaxMt;
+        sz[3] = bf ? R * (D + I) * 2 : 0;
         sz[4] = R * (D / 2 + D / 32);
     } else if (cc.gemm) {
         sz[1] = R * D * 4;
