@@ -390,10 +390,12 @@ int mvllm_hip_bf16_planes(int fmt, int terms, const float *x_dev, int n, int K,
 
 /* MXFP4 activation quantization on the device, bit-exact with fp4_activation_qdq
  * (src/quant/native_act.cpp:159-179) for block 32: rows x [n, K] f32 ->
- * codes [n, K/2] packed e2m1 (low nibble = even k) + scales [n, K/32] ue8m0.
- * K must be a multiple of 32.  Synchronous.  1 ok. */
+ * codes [n, K/2] packed e2m1 (low nibble = even k) + scales [n, K/32] ue8m0, and,
+ * when planes_dev is not NULL, the quantized values themselves as bf16 [n, K] (each is
+ * exact in bf16: the reference's QDQ output rounded to nothing).  K must be a multiple
+ * of 32.  Synchronous.  1 ok. */
 int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
-                             uint8_t *scales_dev);
+                             uint8_t *scales_dev, uint16_t *planes_dev);
 
 /* Memory-system probe used to calibrate the roofline (no reference counterpart):
  * kind 0 streams `bytes` of src_dev with coalesced 16-byte reads, kind 1 copies them to

@@ -2174,7 +2174,7 @@ int mvllm_hip_bf16_planes(int fmt, int terms, const float *x_dev, int n, int K,
 }
 
 int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_dev,
-                             uint8_t *scales_dev) {
+                             uint8_t *scales_dev, uint16_t *planes_dev) {
     Ctx &C = ctx();
     std::lock_guard<std::mutex> lk(C.mu);
     set_err("");
@@ -2182,7 +2182,8 @@ int mvllm_hip_quantize_mxfp4(const float *x_dev, int n, int K, uint8_t *codes_de
         set_err("quantize_mxfp4: bad arguments");
         return 0;
     }
-    HIP_TRY(launch_quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev, C.own));
+    HIP_TRY(launch_quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev, C.own, nullptr,
+                                  planes_dev));
     HIP_TRY(hipStreamSynchronize(C.own));
     return 1;
 }

@@ -57,7 +57,7 @@ _SIGS = {
     "mvllm_hip_stats": (_i, [_p, _i]),
     "mvllm_hip_stats_reset": (None, []),
     "mvllm_hip_dequant": (_i, [_i, _p, _p, _i, _i, _p]),
-    "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p]),
+    "mvllm_hip_quantize_mxfp4": (_i, [_p, _i, _i, _p, _p, _p]),
     "mvllm_hip_bf16_planes": (_i, [_i, _i, _p, _i, _i, _p]),
     "mvllm_hip_router_dev": (_i, [_p, _p, _p, _i, _i, _i, _i, _f, _p, _p, _p, _p, _p]),
     "mvllm_hip_linear_dev": (_i, [_i, _p, _p, _i, _i, _p, _i, _p, _p]),
@@ -311,8 +311,11 @@ def bf16_planes(fmt, terms, x_dev, n, K, planes_dev):
            "mvllm_hip_bf16_planes")
 
 
-def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev):
-    _check(lib().mvllm_hip_quantize_mxfp4(_ptr(x_dev), n, K, _ptr(codes_dev), _ptr(scales_dev)),
+def quantize_mxfp4(x_dev, n, K, codes_dev, scales_dev, planes_dev=None):
+    """MXFP4 codes + ue8m0 scales of x [n, K]; planes_dev (optional, bf16/int16 [n, K]):
+    the quantized values as bf16."""
+    _check(lib().mvllm_hip_quantize_mxfp4(_ptr(x_dev), n, K, _ptr(codes_dev), _ptr(scales_dev),
+                                          _ptr(planes_dev)),
            "mvllm_hip_quantize_mxfp4")
 
 

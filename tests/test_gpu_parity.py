@@ -123,14 +123,21 @@ def test_quantize_mxfp4_bit_exact(hip, orc):
     x[0, :32] = 0.0
     x[1, 5], x[2, 7], x[3, 9] = np.nan, np.inf, -np.inf
     x[4, :32] = np.float32(0.25) * (np.arange(32) % 13)  # exact ties between codes
+    x[5, :32] = np.float32(2.0 ** -130) * (np.arange(32) % 7)  # scale 2^-127, subnormals
     codes = torch.zeros((n, K // 2), dtype=torch.uint8, device="cuda")
     scales = torch.zeros((n, K // 32), dtype=torch.uint8, device="cuda")
-    hip.quantize_mxfp4(dev(x), n, K, codes, scales)
+    planes = torch.full((n, K), -1, dtype=torch.int16, device="cuda")
+    hip.quantize_mxfp4(dev(x), n, K, codes, scales, planes)
     cg, sg = codes.cpu().numpy(), scales.cpu().numpy()
+    pg = planes.cpu().numpy().view(np.uint16)
     for r in range(n):
-        rc, _, sc, cd = orc.fp4_activation_qdq(x[r], 32)
+        rc, q, sc, cd = orc.fp4_activation_qdq(x[r], 32)
         assert np.array_equal(sg[r], sc), r
         assert np.array_equal(npref.unpack_nibbles(cg[r:r + 1], K)[0], cd), r
+        # the bf16 copy of the reference's QDQ output: exact (its low half is zero)
+        qb = q.view(np.uint32)
+        assert np.all((qb & 0xffff) == 0), r
+        assert np.array_equal(pg[r], (qb >> 16).astype(np.uint16)), r
 
 
 @pytest.mark.parametrize("fmt", [4, 7])
