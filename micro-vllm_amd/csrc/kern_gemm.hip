@@ -108,25 +108,26 @@ struct TaskD {
 
 // One workgroup per task.  UNI: one expert (A.ew1) over rows [0, A.nrows_all) in blocks of
 // BM, no item list (dense linears; a template parameter so that the selection costs the
-// grouped form no registers).  The 32-row class with one term is held to 128 VGPRs (4 waves per SIMD), so two
-// workgroups share a CU: it needs 126-131 VGPRs, and the cap costs at most a few spilled
-// registers.  Measured on c3: 1.60 -> 1.53 ms per call.
+// grouped form no registers).  The 32-row class with one term is held to 128 VGPRs (4 waves
+// per SIMD), so two workgroups share a CU: the grouped form needs 110-120 (its A tiles go
+// straight into LDS), the dense-linear form 126-131, where the cap costs at most a few
+// spilled registers (c3 with register-staged A tiles: 1.60 -> 1.53 ms per call).
 template <int FMT, bool DUAL, int TERMS, int MT, bool UNI>
 __global__ __launch_bounds__(kGemmThreads)
 __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
-    // scales in 64-byte chunks (GScaleC) where the registers allow
-    // (not the MXFP4 down kernel of the 16-row class: it would pass 128 VGPRs)
-    constexpr bool kChunkS = !UNI && TERMS == 1 &&
-                             (MT == 4 || (MT == 1 && (DUAL || FMT == 4)));
+    // scales in 64-byte chunks (GScaleC) where the registers allow (not the MXFP4 down
+    // kernel of the 32-row class: it would pass its 128-VGPR cap and spill)
+    constexpr bool kChunkS = !UNI && TERMS == 1 && MT <= 4 && !(FMT == 7 && !DUAL && MT == 2);
     constexpr int PPC = gscale_ppc<FMT>();
     using Scl = std::conditional_t<kChunkS, GScaleC, GScale<FMT>>;
     constexpr int BM = 16 * MT;
     constexpr int PA = MT >= 8 ? 1 : 2;  // activation prefetch distance in K steps
-    // The one-term 128-row class loads its A tiles straight into LDS (buffer_load ... lds):
-    // no staging registers.  Its rows are then 512 bytes apart without padding, and a
-    // row's 16-byte chunks are XOR-swizzled by the row's low four bits, which keeps the
-    // fragment reads free of bank conflicts.
-    constexpr bool kDmaA = MT == 8 && TERMS == 1 && !UNI;
+    // The one-term classes load their A tiles straight into LDS (buffer_load ... lds): no
+    // staging registers.  Rows are then 512 bytes apart without padding, and a row's
+    // 16-byte chunks are XOR-swizzled by the row's low four bits, which keeps the fragment
+    // reads free of bank conflicts (the padded layout staged through registers spent
+    // 14-20 % of the 16/32/64-row classes' CU cycles in LDS bank conflicts).
+    constexpr bool kDmaA = TERMS == 1 && !UNI;
     constexpr int APITCH = kDmaA ? kGemmBK * 2 : kGemmPitch;  // LDS bytes per A row
     constexpr int PL = BM * APITCH;                  // bytes per plane per stage
     constexpr int STAGE = kDmaA ? TERMS * PL : gemm_stage_bytes(FMT, TERMS, MT);
@@ -248,8 +249,8 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
     };
 
     // kDmaA: the A tile of step k into LDS buffer buf.  DMA load i of wave w fills LDS rows
-    // 16 w + 2 i and + 1 (lane l: row + l / 32, physical chunk l % 32, which holds logical
-    // chunk (l % 32) ^ (row % 16)).  The item's rows are one buffer resource: rows past
+    // (BM / 8) w + 2 i and + 1 (lane l: row + l / 32, physical chunk l % 32, which holds
+    // logical chunk (l % 32) ^ (row % 16)).  The item's rows are one buffer resource: rows past
     // nrow lie beyond it and load as zeros (their results are never stored).
     auto dma_a = [&] __attribute__((always_inline)) (const TaskD<FMT> &d, int k, int buf) {
         if constexpr (kDmaA) {
@@ -258,12 +259,12 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
             const int dr = lane >> 5, pc = lane & 31;
 #pragma unroll
             for (int i = 0; i < BM * APITCH / 1024 / 8; ++i) {
-                const int r = 16 * wave + 2 * i + dr;
-                const int lc = pc ^ ((2 * i + dr) & 15);
+                const int r = (BM / 8) * wave + 2 * i + dr;
+                const int lc = pc ^ (r & 15);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(
                     ra,
                     (__attribute__((address_space(3))) void *)(smem + buf * STAGE +
-                                                              (8 * wave + i) * 1024),
+                                                              ((BM / 16) * wave + i) * 1024),
                     16, (uint32_t)r * (uint32_t)K * 2u + 16u * (uint32_t)lc,
                     (uint32_t)k * (uint32_t)(kGemmBK * 2), 0, 0);
             }
