@@ -121,3 +121,56 @@ def test_prefill_full_size(hip, orc, name, T):
             acc = (acc + (np.float32(w.rw[j]) * yall[j]).astype(np.float32)).astype(np.float32)
         assert np.array_equal(acc.view(np.uint32), outg[t].view(np.uint32)), t
     say(f"  combine bit-exact on {len(toks)} tokens")
+
+
+def test_prefill_full_size_fp4act(hip, orc):
+    """c4 at its full size with native MXFP4 activations (option fp4act): the heavy experts
+    through the scaled-FP4 kernel in 64-row blocks, the 16/32-row classes through the bf16
+    GEMM on exact bf16 copies of the quantized activations.  Sampled rows (as above) against
+    the composed oracle (fp4_activation_qdq on x and H around the f32 moe_block maths,
+    nb = 1 on those rows), with the native-FP4 bar: products are exact, so only the
+    summation order differs, except where it moves an h value across an e2m1 rounding
+    boundary (rare; one code step of one h element)."""
+    from mvllm_hip import synth
+    name, T = "c4", 2048
+    say("prefill full size fp4act", name, T)
+    w = synth.make_workload(name, T=T, with_experts=False)
+    D, I, fmt = w.D, w.I, w.fmt
+    R = int(w.nr.sum())
+    geom = hip.expert_geom(fmt, D, I)
+    pool, stride = synth.device_pool(torch, fmt, D, I, w.nb, 4321 + T, geom)
+    off = geom[1]
+    base = pool.data_ptr()
+    order = (0, 2, 4, 1, 3, 5)
+    ptrs = [[base + i * stride + int(off[o]) for i in range(w.nb)] for o in order]
+    xg = torch.from_numpy(w.xg).cuda()
+    y = torch.zeros((R, D), dtype=torch.float32, device="cuda")
+    assert hip.set_option("fp4act", 1)
+    try:
+        hip.moe_block_dev(w.nb, D, I, fmt, *ptrs, xg, w.xoff, w.nr,
+                          np.arange(R, dtype=np.int32), np.ones(R, np.float32), y, R, w.act,
+                          w.a, w.b)
+        torch.cuda.synchronize()
+    finally:
+        hip.set_option("fp4act", 0)
+    rng = np.random.default_rng(12)
+    picks = sample_rows(w.nr, w.xoff, rng)
+    gots, exps = [], []
+    for e, rs in picks.items():
+        j = int(w.xoff[e]) + np.asarray(rs, np.int64)
+        gp, up, dp, gs, us, ds = synth.blob_pieces(pool[e].cpu().numpy(), fmt, D, I, off)
+        exp = np.zeros((len(rs), D), np.float32)
+        assert orc.moe_block_fp4act(1, D, I, fmt, [gp], [up], [dp], [gs], [us], [ds], w.xg[j],
+                                    np.zeros(1, np.int32), np.array([len(rs)], np.int32),
+                                    np.arange(len(rs), dtype=np.int32),
+                                    np.ones(len(rs), np.float32), exp, len(rs), w.act, w.a,
+                                    w.b) == 1
+        gots.append(y[torch.from_numpy(j).cuda()].cpu().numpy())
+        exps.append(exp)
+    got, exp = np.concatenate(gots), np.concatenate(exps)
+    den = np.max(np.abs(exp))
+    dev_ = np.abs(got.astype(np.float64) - exp) / den
+    say(f"  {got.shape[0]} rows of {len(picks)} experts: rel_err max {float(dev_.max()):.2e}, "
+        f"p99 {float(np.quantile(dev_, 0.99)):.2e}")
+    assert float(dev_.max()) < 1e-2
+    assert float(np.quantile(dev_, 0.99)) < 1e-5
