@@ -53,8 +53,13 @@ __host__ __device__ constexpr int f4_stage_bytes(int mt) {
 size_t fp4_lds_bytes(int mt) { return 2 * (size_t)f4_stage_bytes(mt); }
 
 struct F4Step {
-    u32x4 w[2][2];  // tile m, MFMA step s: row t, bytes 64 s + 16 q of the 128-byte step
-    u32x2 s[2];     // tile m: row t's 8 scale bytes of the step
+    u32x4 w[2][2];  // tile m, MFMA step s: row t, bytes 32 q + 16 s of the 128-byte step
+};
+// Weight scales in 64-byte chunks of each row (8 steps): lane (t, q) holds bytes 16 q ..
+// 16 q + 15 of row t's chunk, i.e. steps 2 q and 2 q + 1 of it.  One load per 8 steps:
+// per-step 8-byte loads made a third of the kernel's L2 requests.
+struct F4Scl {
+    u32x4 c[2];
 };
 
 template <bool DUAL, int MT>
@@ -62,13 +67,20 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int BM = 16 * MT;
     constexpr int STAGE = f4_stage_bytes(MT);
     constexpr int CCH = (BM * 8 + kF4Threads - 1) / kF4Threads;  // 16-byte code chunks/thread
-    constexpr int PA = MT >= 8 ? 1 : 2;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int n_tasks = (int)gridDim.x;
     const int task = A.xcd ? xcd_task(blockIdx.x, n_tasks) : (int)blockIdx.x;
-    const int item = task / A.nbn;
-    const int nb = task - item * A.nbn;
+    // An expert's run of nblk items owns tasks [g0 nbn, (g0 + nblk) nbn); they go column
+    // block by column block, its row blocks adjacent, so that the row blocks running side
+    // by side on one XCD read that column block's weights through its L2 together.
+    int item = task / A.nbn;
+    const int grp = A.items[item].pad;  // index in the run << 16 | run length (0: alone)
+    const int nblk = max(grp & 0xffff, 1);
+    const int g0 = item - (grp >> 16);
+    const int local = task - g0 * A.nbn;
+    const int nb = local / nblk;
+    item = g0 + (local - nb * nblk);
     const F4Item it = A.items[item];
     const ExpertWork &ew = A.ew[it.a];
     const int K = A.K, O = A.O, nrow = it.nrow;
@@ -87,8 +99,8 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
         const int trow = DUAL ? col0 : col0 + 16 * m;
         rw[m] = buf_rsrc(ew.w[mi], (uint32_t)O * rowb);
         rs[m] = buf_rsrc(ew.s[mi], (uint32_t)O * srow);
-        vw[m] = (uint32_t)(trow + t) * rowb + 16u * (uint32_t)q;
-        vs[m] = (uint32_t)(trow + t) * srow;
+        vw[m] = (uint32_t)(trow + t) * rowb + 32u * (uint32_t)q;
+        vs[m] = (uint32_t)(trow + t) * srow + 16u * (uint32_t)q;
     }
     auto load_b = [&] __attribute__((always_inline)) (F4Step &b, int k) {
 #pragma unroll
@@ -96,15 +108,27 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
 #pragma unroll
             for (int s = 0; s < 2; ++s)
                 b.w[m][s] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[m], vw[m] + 64 * s,
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw[m], vw[m] + 16 * s,
                                                                  (uint32_t)k * 128u, 0));
-            b.s[m] = __builtin_bit_cast(
-                u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs[m], vs[m], (uint32_t)k * 8u, 0));
         }
+    };
+    // the scale chunk holding step k, loaded only when step k opens it (otherwise the
+    // offset lies past the buffer: zeros, no memory access, no branch around the load)
+    auto load_s = [&] __attribute__((always_inline)) (F4Scl &sc, int k) {
+        const bool open = (k & 7) == 0;
+#pragma unroll
+        for (int m = 0; m < 2; ++m)
+            sc.c[m] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           rs[m], open ? vs[m] + (uint32_t)(k >> 3) * 64u : 0xffffff00u, 0, 0));
     };
 
     // A staging: code chunk c -> row c / 8, 16-byte column c % 8; scales: thread r < BM
-    // takes row r's 8 bytes.  Rows past nrow re-read the last row (never stored).
+    // takes row r's 8 bytes (the other threads' offsets lie past the buffer).  Rows past
+    // nrow re-read the last row (never stored).
+    const __amdgpu_buffer_rsrc_t ras =
+        buf_rsrc(A.ascale + (size_t)jbase * srow, (uint32_t)nrow * srow);
+    const uint32_t vas = tid < BM ? (uint32_t)min(tid, nrow - 1) * srow : 0xffffff00u;
     struct AStage {
         u32x4 v[CCH];
         u32x2 sc;
@@ -117,9 +141,8 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             ra.v[u] = *reinterpret_cast<const u32x4 *>(A.acode + (size_t)(jbase + r) * rowb +
                                                        (size_t)k * 128 + 16 * cc);
         }
-        const int r = min(tid % BM, nrow - 1);
-        ra.sc = *reinterpret_cast<const u32x2 *>(A.ascale + (size_t)(jbase + r) * srow +
-                                                 (size_t)k * 8);
+        ra.sc = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(ras, vas, (uint32_t)k * 8u, 0));
     };
     auto store_a = [&] __attribute__((always_inline)) (const AStage &ra, int buf) {
         char *base = smem + buf * STAGE;
@@ -138,9 +161,20 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     for (int mt = 0; mt < MT; ++mt)
         acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&] __attribute__((always_inline)) (const F4Step &b, int buf) {
-        const char *base = smem + buf * STAGE;
+    // step k (parity P = k % 2) on LDS buffer P: step k's 8 scale bytes of row t sit in
+    // lane (t, (k % 8) / 2), words 2 P and 2 P + 1
+    auto compute = [&] __attribute__((always_inline)) (const F4Step &b, const F4Scl &sc, int k,
+                                                        auto par) {
+        constexpr int P = decltype(par)::value;
+        const char *base = smem + P * STAGE;
         const uint8_t *lsc = reinterpret_cast<const uint8_t *>(base + BM * kF4Pitch);
+        const int src = 4 * (t + 16 * ((k & 7) >> 1));
+        uint32_t sw[2][2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            sw[m][0] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)sc.c[m][2 * P]);
+            sw[m][1] = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)sc.c[m][2 * P + 1]);
+        }
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             i32x8 bv[2];
@@ -149,17 +183,17 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             for (int m = 0; m < 2; ++m) {
                 const u32x4 w = b.w[m][s];
                 bv[m] = i32x8{(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
-                const int blk = 4 * s + q;  // this lane's 32-block among the step's 8
-                const uint32_t word = blk < 4 ? b.s[m].x : b.s[m].y;
+                const int blk = 2 * q + s;  // this lane's 32-block among the step's 8
+                const uint32_t word = q < 2 ? sw[m][0] : sw[m][1];
                 sb[m] = (int)((word >> (8 * (blk & 3))) & 0xffu);
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const int row = mt * 16 + t;
-                const u32x4 av = *reinterpret_cast<const u32x4 *>(base + row * kF4Pitch + 64 * s +
-                                                                  16 * q);
+                const u32x4 av = *reinterpret_cast<const u32x4 *>(base + row * kF4Pitch + 32 * q +
+                                                                  16 * s);
                 const i32x8 a8 = i32x8{(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
-                const int sa = (int)lsc[row * 8 + 4 * s + q];
+                const int sa = (int)lsc[row * 8 + 2 * q + s];
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
                     acc[mt][m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -168,36 +202,35 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
         }
     };
 
-    // pipeline as the bf16 grouped GEMM (weights two steps ahead, activations staged one
-    // step ahead from registers loaded PA steps ahead; no branches around the loads;
-    // prefetches past the last step read that step again)
+    // pipeline as the bf16 grouped GEMM: weights two steps ahead, activations staged one
+    // step ahead from registers loaded two steps ahead, scale chunks two steps ahead of
+    // the step that opens them; no branches around the loads; prefetches past the last
+    // step read that step again
     const int nk = K / 256;
     F4Step b0, b1;
+    F4Scl sc, sn;  // scale chunk of this step / the next chunk
     AStage ra0, ra1;
     load_a(ra0, 0);
-    if constexpr (PA == 2)
-        load_a(ra1, min(1, nk - 1));
+    load_a(ra1, min(1, nk - 1));
     load_b(b0, 0);
+    load_s(sn, 0);
     load_b(b1, min(1, nk - 1));
     store_a(ra0, 0);
     __syncthreads();
     for (int k = 0; k < nk; k += 2) {
-        if constexpr (PA == 2)
-            load_a(ra0, min(k + 2, nk - 1));
-        else
-            load_a(ra1, min(k + 1, nk - 1));
-        compute(b0, 0);
+        if ((k & 7) == 0)
+            sc = sn;
+        load_a(ra0, min(k + 2, nk - 1));
+        compute(b0, sc, k, std::integral_constant<int, 0>{});
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, min(k + 2, nk - 1));  // past the end: the last step again (L2 hits)
+        load_b(b0, min(k + 2, nk - 1));
+        load_s(sn, min(k + 2, nk - 1));
         store_a(ra1, 1);
         __syncthreads();
         if (k + 1 >= nk)
             break;
-        if constexpr (PA == 2)
-            load_a(ra1, min(k + 3, nk - 1));
-        else
-            load_a(ra0, min(k + 2, nk - 1));
-        compute(b1, 1);
+        load_a(ra1, min(k + 3, nk - 1));
+        compute(b1, sc, k + 1, std::integral_constant<int, 1>{});
         __builtin_amdgcn_sched_barrier(0);
         load_b(b1, min(k + 3, nk - 1));
         store_a(ra0, 0);

@@ -499,6 +499,21 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     if (split >= P.ew.size())
         for (int c = 0; c < 4; ++c)
             split_at[c] = per[c].size();
+    // 4th word: (block index within the expert's run of items in this class) << 16 | run
+    // length; the scaled-FP4 kernel orders an expert's tasks column block by column block
+    // with these (runs of 2^15 blocks or more stay one item per run)
+    for (int c = 0; c < 4; ++c) {
+        std::vector<int> &v = per[c];
+        for (size_t j = 0; j < v.size();) {
+            size_t e = j;
+            while (e < v.size() && v[e] == v[j])
+                e += 4;
+            const int n = static_cast<int>((e - j) / 4);
+            for (int r = 0; r < n; ++r)
+                v[j + 4 * r + 3] = n < 0x8000 ? (r << 16) | n : 1;
+            j = e;
+        }
+    }
     cc.items.clear();
     cc.n_gcls = 0;
     for (int c = 0; c < 4; ++c) {
