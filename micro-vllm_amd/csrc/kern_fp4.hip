@@ -12,14 +12,16 @@
 // first -- and the lane's scale operand is the ue8m0 byte of that 32-block; the result
 // is C[4 q + i][t], i = 0..3, as for the bf16 16x16 MFMAs.
 //
-// Tiling as the bf16 grouped GEMM (row tiles MT = 1, 2 or 4: the 128-row class spills):
-// a workgroup of 8 waves serves (item, column block),
-// each wave two 16-column tiles (gate and up at the same columns for the dual
-// projection, two adjacent tiles of the down matrix otherwise) over MT row tiles; K
-// advances 256 per step; the item's activation codes and scales of a step are staged in
-// LDS (double buffered, registers loaded two steps ahead), the weights of a step are
-// loaded two steps ahead into registers: per tile and lane two 16-byte loads (row t,
-// bytes 64 s + 16 q) and one 8-byte scale load (row t, the step's 8 blocks).
+// Tiling as the bf16 grouped GEMM (row tiles MT = 4 or 8; the 16- and 32-row classes
+// take the bf16 GEMM on exact bf16 copies of the quantized activations): a workgroup of 8
+// waves serves (item, column block), each wave two 16-column tiles (gate and up at the same
+// columns for the dual projection, two adjacent tiles of the down matrix otherwise) over
+// MT row tiles; K advances 256 per step.  The item's activation codes of a step go
+// straight into LDS (buffer_load ... lds, double buffered, one step ahead), their scales
+// through registers; the weights of a step are loaded two steps ahead into registers (per
+// tile and lane two 16-byte loads: row t, bytes 32 q + 16 s), their scales in 64-byte
+// chunks per 8 steps.  MFMA step s takes 32-block 2 q + s of the 256-K step in lane
+// (t, q) (A and B agree on the order, which only permutes the summation).
 #include "mfma_common.h"
 
 namespace mvllm_hip {
@@ -44,10 +46,10 @@ struct F4Args {
 };
 
 constexpr int kF4Threads = 512;
-constexpr int kF4Pitch = 128 + 16;  // LDS bytes per A row of codes (+16: banks)
+constexpr int kF4Row = 128;  // LDS bytes per A row of codes (a step of 256 K)
 
 __host__ __device__ constexpr int f4_stage_bytes(int mt) {
-    return 16 * mt * kF4Pitch + 16 * mt * 8;
+    return 16 * mt * kF4Row + 16 * mt * 8;
 }
 
 size_t fp4_lds_bytes(int mt) { return 2 * (size_t)f4_stage_bytes(mt); }
@@ -66,7 +68,6 @@ template <bool DUAL, int MT>
 __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int BM = 16 * MT;
     constexpr int STAGE = f4_stage_bytes(MT);
-    constexpr int CCH = (BM * 8 + kF4Threads - 1) / kF4Threads;  // 16-byte code chunks/thread
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int n_tasks = (int)gridDim.x;
@@ -123,37 +124,36 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
                            rs[m], open ? vs[m] + (uint32_t)(k >> 3) * 64u : 0xffffff00u, 0, 0));
     };
 
-    // A staging: code chunk c -> row c / 8, 16-byte column c % 8; scales: thread r < BM
-    // takes row r's 8 bytes (the other threads' offsets lie past the buffer).  Rows past
-    // nrow re-read the last row (never stored).
+    // A codes of step k into LDS buffer buf straight from memory (buffer_load ... lds), no
+    // staging registers.  DMA load i of wave w fills rows 8 (w BM / 64 + i) .. + 7 (lane l:
+    // row + l / 8, physical chunk l % 8, which holds logical chunk (l % 8) ^ ((row / 2) %
+    // 8)): the fragment reads of 16 rows then hit 16 distinct bank groups.  The item's
+    // rows are one buffer resource: rows past nrow load as zeros (never stored).
+    const __amdgpu_buffer_rsrc_t rac =
+        buf_rsrc(A.acode + (size_t)jbase * rowb, (uint32_t)nrow * rowb);
+    auto dma_a = [&] __attribute__((always_inline)) (int k, int buf) {
+#pragma unroll
+        for (int i = 0; i < BM / 64; ++i) {
+            const int g = wave * (BM / 64) + i;
+            const int r = 8 * g + (lane >> 3);
+            const int lc = (lane & 7) ^ ((r >> 1) & 7);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rac, (__attribute__((address_space(3))) void *)(smem + buf * STAGE + g * 1024),
+                16, (uint32_t)r * rowb + 16u * (uint32_t)lc, (uint32_t)k * 128u, 0, 0);
+        }
+    };
+    // A scales: thread r < BM takes row r's 8 bytes of the step (the other threads'
+    // offsets lie past the buffer: no memory access)
     const __amdgpu_buffer_rsrc_t ras =
         buf_rsrc(A.ascale + (size_t)jbase * srow, (uint32_t)nrow * srow);
-    const uint32_t vas = tid < BM ? (uint32_t)min(tid, nrow - 1) * srow : 0xffffff00u;
-    struct AStage {
-        u32x4 v[CCH];
-        u32x2 sc;
-    };
-    auto load_a = [&] __attribute__((always_inline)) (AStage &ra, int k) {
-#pragma unroll
-        for (int u = 0; u < CCH; ++u) {
-            const int c = u * kF4Threads + tid;
-            const int r = min((c >> 3) % BM, nrow - 1), cc = c & 7;
-            ra.v[u] = *reinterpret_cast<const u32x4 *>(A.acode + (size_t)(jbase + r) * rowb +
-                                                       (size_t)k * 128 + 16 * cc);
-        }
-        ra.sc = __builtin_bit_cast(
+    const uint32_t vas = tid < BM ? (uint32_t)tid * srow : 0xffffff00u;
+    auto load_as = [&] __attribute__((always_inline)) (int k) {
+        return __builtin_bit_cast(
             u32x2, __builtin_amdgcn_raw_buffer_load_b64(ras, vas, (uint32_t)k * 8u, 0));
     };
-    auto store_a = [&] __attribute__((always_inline)) (const AStage &ra, int buf) {
-        char *base = smem + buf * STAGE;
-#pragma unroll
-        for (int u = 0; u < CCH; ++u) {
-            const int c = u * kF4Threads + tid;
-            if (c < BM * 8)
-                *reinterpret_cast<u32x4 *>(base + (c >> 3) * kF4Pitch + 16 * (c & 7)) = ra.v[u];
-        }
+    auto store_as = [&] __attribute__((always_inline)) (u32x2 v, int buf) {
         if (tid < BM)
-            *reinterpret_cast<u32x2 *>(base + BM * kF4Pitch + 8 * tid) = ra.sc;
+            *reinterpret_cast<u32x2 *>(smem + buf * STAGE + BM * kF4Row + 8 * tid) = v;
     };
 
     f4v acc[MT][2];
@@ -161,13 +161,17 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     for (int mt = 0; mt < MT; ++mt)
         acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
 
+    // this lane's LDS offsets in a stage: row t's chunk 2 q + s of the codes (swizzled; rows
+    // 16 mt + t add 16 mt rows, which keep the swizzle), and its scale byte 2 q
+    const int ao0 = t * kF4Row + 16 * ((2 * q) ^ ((t >> 1) & 7));
+    const int ao1 = t * kF4Row + 16 * ((2 * q + 1) ^ ((t >> 1) & 7));
+    const int so = BM * kF4Row + 8 * t + 2 * q;
     // step k (parity P = k % 2) on LDS buffer P: step k's 8 scale bytes of row t sit in
     // lane (t, (k % 8) / 2), words 2 P and 2 P + 1
     auto compute = [&] __attribute__((always_inline)) (const F4Step &b, const F4Scl &sc, int k,
                                                         auto par) {
         constexpr int P = decltype(par)::value;
         const char *base = smem + P * STAGE;
-        const uint8_t *lsc = reinterpret_cast<const uint8_t *>(base + BM * kF4Pitch);
         const int src = 4 * (t + 16 * ((k & 7) >> 1));
         uint32_t sw[2][2];
 #pragma unroll
@@ -189,11 +193,11 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const int row = mt * 16 + t;
-                const u32x4 av = *reinterpret_cast<const u32x4 *>(base + row * kF4Pitch + 32 * q +
-                                                                  16 * s);
+                // row tile mt: constant offsets from this lane's addresses (ds immediates)
+                const u32x4 av = *reinterpret_cast<const u32x4 *>(base + (s ? ao1 : ao0) +
+                                                                  mt * 16 * kF4Row);
                 const i32x8 a8 = i32x8{(int)av.x, (int)av.y, (int)av.z, (int)av.w, 0, 0, 0, 0};
-                const int sa = (int)lsc[row * 8 + 2 * q + s];
+                const int sa = (int)(uint8_t)base[so + mt * 16 * 8 + s];
 #pragma unroll
                 for (int m = 0; m < 2; ++m)
                     acc[mt][m] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
@@ -202,38 +206,55 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
         }
     };
 
-    // pipeline as the bf16 grouped GEMM: weights two steps ahead, activations staged one
-    // step ahead from registers loaded two steps ahead, scale chunks two steps ahead of
-    // the step that opens them; no branches around the loads; prefetches past the last
-    // step read that step again
+    // pipeline as the bf16 grouped GEMM: weights two steps ahead, activation codes one
+    // step ahead (issued first: the barrier waits for them only), activation scales
+    // staged one step ahead from registers loaded two steps ahead, weight-scale chunks two
+    // steps ahead of the step that opens them; no branches around the loads; prefetches
+    // past the last step read that step again
+    // The step's MFMAs complete before the next loads of its weight registers are issued:
+    // left free, the compiler sank them below the loads and the barrier and held three
+    // sets of weight registers (the 128-row form then spilled).
+    auto pin_acc = [&] __attribute__((always_inline)) () {
+        if constexpr (MT == 8)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+                asm volatile("" : "+v"(acc[mt][m]));
+    };
     const int nk = K / 256;
     F4Step b0, b1;
     F4Scl sc, sn;  // scale chunk of this step / the next chunk
-    AStage ra0, ra1;
-    load_a(ra0, 0);
-    load_a(ra1, min(1, nk - 1));
+    u32x2 as0, as1;
+    dma_a(0, 0);
+    as0 = load_as(0);
     load_b(b0, 0);
     load_s(sn, 0);
+    as1 = load_as(min(1, nk - 1));
     load_b(b1, min(1, nk - 1));
-    store_a(ra0, 0);
+    store_as(as0, 0);
     __syncthreads();
     for (int k = 0; k < nk; k += 2) {
         if ((k & 7) == 0)
             sc = sn;
-        load_a(ra0, min(k + 2, nk - 1));
+        dma_a(min(k + 1, nk - 1), 1);
+        as0 = load_as(min(k + 2, nk - 1));
         compute(b0, sc, k, std::integral_constant<int, 0>{});
+        pin_acc();
         __builtin_amdgcn_sched_barrier(0);
         load_b(b0, min(k + 2, nk - 1));
         load_s(sn, min(k + 2, nk - 1));
-        store_a(ra1, 1);
+        store_as(as1, 1);
         __syncthreads();
         if (k + 1 >= nk)
             break;
-        load_a(ra1, min(k + 3, nk - 1));
+        dma_a(min(k + 2, nk - 1), 0);
+        as1 = load_as(min(k + 3, nk - 1));
         compute(b1, sc, k + 1, std::integral_constant<int, 1>{});
+        pin_acc();
         __builtin_amdgcn_sched_barrier(0);
         load_b(b1, min(k + 3, nk - 1));
-        store_a(ra0, 0);
+        store_as(as0, 0);
         __syncthreads();
     }
 
@@ -293,9 +314,8 @@ hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *
     a.act_b = act_b;
 #define MVLLM_F4(D_)                                                                          \
     switch (mt) {                                                                             \
-    case 1: return launch_f4_t<D_, 1>(a, n_items, st);                                        \
-    case 2: return launch_f4_t<D_, 2>(a, n_items, st);                                        \
     case 4: return launch_f4_t<D_, 4>(a, n_items, st);                                        \
+    case 8: return launch_f4_t<D_, 8>(a, n_items, st);                                        \
     default: return hipErrorInvalidValue;                                                     \
     }
     if (dual) {
