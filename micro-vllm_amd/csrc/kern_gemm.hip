@@ -152,8 +152,20 @@ __attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_ge
 
     auto make_task = [&] __attribute__((always_inline)) (int task) {
         TaskD<FMT> d;
-        const int item = task / A.nbn;
-        const int nb = task - item * A.nbn;
+        int item = task / A.nbn;
+        int nb = task - item * A.nbn;
+        if constexpr (!UNI && MT <= 2) {
+            // An expert's run of nblk items owns tasks [g0 nbn, (g0 + nblk) nbn); they go
+            // column block by column block, its row blocks adjacent, so that the row blocks
+            // running side by side on one XCD read that column block's weights through its
+            // L2 together (item word 3: index in the run << 16 | run length, 0: alone).
+            const int grp = A.items[item].pad;
+            const int nblk = max(grp & 0xffff, 1);
+            const int g0 = item - (grp >> 16);
+            const int local = task - g0 * A.nbn;
+            nb = local / nblk;
+            item = g0 + (local - nb * nblk);
+        }
         GemmItem it;
         if constexpr (UNI) {
             it.a = 0;

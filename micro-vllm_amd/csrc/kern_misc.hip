@@ -144,15 +144,16 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
             for (int o = 4; o >= 1; o >>= 1)
                 amax = fmaxf(amax, __shfl_xor(amax, o, 8));
             amax = fmaxf(amax, 6.f * 1.1754943508222875e-38f);  // 6 * 2^-126
-            int ex = ceil_log2_normal(amax / 6.f);
-            ex = ex < -127 ? -127 : (ex > 127 ? 127 : ex);
-            // x / 2^ex == x * 2^-ex exactly (both round the same real number); 2^-127 is
-            // subnormal, so that one case divides
+            // amax / 6 lies in [2^-126, FLT_MAX / 6 < 2^126] or is +Inf (exponent 0), so
+            // ex is within [-126, 126] and the reference's clamp to [-127, 127] never
+            // binds; 2^-ex is then a normal float and x / 2^ex == x * 2^-ex exactly (both
+            // round the same real number)
+            const int ex = ceil_log2_normal(amax / 6.f);
             const float inv = __uint_as_float((uint32_t)(127 - ex) << 23);
             uint32_t packed = 0;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float sc = ex == 127 ? f[i] / ldexpf(1.f, 127) : f[i] * inv;
+                const float sc = f[i] * inv;
                 const float q = fmaxf(-6.f, fminf(6.f, sc));
                 packed |= (uint32_t)nearest_e2m1(q) << (4 * i);
             }

@@ -482,6 +482,9 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     cc.terms = cc.terms >= 2 ? 2 : 1;
     const int max_mt = cc.f32 ? 4 : cc.fp4 ? kFp4MaxMt : gemm_max_mt(fmt, cc.terms);
     const int bm = 16 * max_mt;
+    // bf16 one-term GEMM: an expert of 33-64 rows (a last block of that size) runs as two
+    // 32-row items of the two-workgroups-per-CU class, which read its weights together
+    const bool split64 = !cc.f32 && !cc.fp4 && cc.terms == 1 && max_mt >= 4;
     std::vector<int> per[4];  // class index = log2(mt)
     size_t split_at[4] = {0, 0, 0, 0};
     for (size_t i = 0; i < P.ew.size(); ++i) {
@@ -491,6 +494,11 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
         const int n = P.ew[i].nrows;
         for (int r0 = 0; r0 < n; r0 += bm) {
             const int nrow = std::min(bm, n - r0);
+            if (split64 && nrow > 32 && nrow <= 64) {
+                per[1].insert(per[1].end(), {static_cast<int>(i), r0, 32, 0,
+                                             static_cast<int>(i), r0 + 32, nrow - 32, 0});
+                continue;
+            }
             const int mt = nrow <= 16 ? 1 : nrow <= 32 ? 2 : nrow <= 64 ? 4 : 8;
             const int c = mt == 1 ? 0 : mt == 2 ? 1 : mt == 4 ? 2 : 3;
             per[c].insert(per[c].end(), {static_cast<int>(i), r0, nrow, 0});
