@@ -68,6 +68,10 @@ template <bool DUAL, int MT>
 __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int BM = 16 * MT;
     constexpr int STAGE = f4_stage_bytes(MT);
+    // steps of weights in flight (128 rows: three, faster than two or four) and the loop
+    // unroll, a multiple of NB and of 2
+    constexpr int NB = MT == 8 ? 3 : 2;
+    constexpr int UN = NB % 2 ? 2 * NB : NB;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int n_tasks = (int)gridDim.x;
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
         }
     };
 
-    // pipeline as the bf16 grouped GEMM: weights two steps ahead, activation codes one
+    // pipeline as the bf16 grouped GEMM: weights NB steps ahead, activation codes one
     // step ahead (issued first: the barrier waits for them only), activation scales
     // staged one step ahead from registers loaded two steps ahead, weight-scale chunks two
     // steps ahead of the step that opens them; no branches around the loads; prefetches
@@ -223,39 +227,41 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
                 asm volatile("" : "+v"(acc[mt][m]));
     };
     const int nk = K / 256;
-    F4Step b0, b1;
+    F4Step b[NB];
     F4Scl sc, sn;  // scale chunk of this step / the next chunk
-    u32x2 as0, as1;
+    u32x2 as[2];
     dma_a(0, 0);
-    as0 = load_as(0);
-    load_b(b0, 0);
+    as[0] = load_as(0);
+    load_b(b[0], 0);
     load_s(sn, 0);
-    as1 = load_as(min(1, nk - 1));
-    load_b(b1, min(1, nk - 1));
-    store_as(as0, 0);
+    as[1] = load_as(min(1, nk - 1));
+#pragma unroll
+    for (int j = 1; j < NB; ++j)
+        load_b(b[j], min(j, nk - 1));
+    store_as(as[0], 0);
     __syncthreads();
-    for (int k = 0; k < nk; k += 2) {
-        if ((k & 7) == 0)
-            sc = sn;
-        dma_a(min(k + 1, nk - 1), 1);
-        as0 = load_as(min(k + 2, nk - 1));
-        compute(b0, sc, k, std::integral_constant<int, 0>{});
-        pin_acc();
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, min(k + 2, nk - 1));
-        load_s(sn, min(k + 2, nk - 1));
-        store_as(as1, 1);
-        __syncthreads();
-        if (k + 1 >= nk)
-            break;
-        dma_a(min(k + 2, nk - 1), 0);
-        as1 = load_as(min(k + 3, nk - 1));
-        compute(b1, sc, k + 1, std::integral_constant<int, 1>{});
-        pin_acc();
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, min(k + 3, nk - 1));
-        store_as(as0, 0);
-        __syncthreads();
+    for (int k = 0; k < nk; k += UN) {
+#pragma unroll
+        for (int j = 0; j < UN; ++j) {  // step k + j: LDS buffer j % 2, weights b[j % NB]
+            const int kk = k + j;
+            if (j > 0 && kk >= nk)
+                break;
+            if (j % 2 == 0 && (kk & 7) == 0)
+                sc = sn;
+            dma_a(min(kk + 1, nk - 1), (j & 1) ^ 1);
+            as[j & 1] = load_as(min(kk + 2, nk - 1));
+            if (j & 1)
+                compute(b[j % NB], sc, kk, std::integral_constant<int, 1>{});
+            else
+                compute(b[j % NB], sc, kk, std::integral_constant<int, 0>{});
+            pin_acc();
+            __builtin_amdgcn_sched_barrier(0);
+            load_b(b[j % NB], min(kk + NB, nk - 1));
+            if (j % 2 == 0)
+                load_s(sn, min(kk + 2, nk - 1));
+            store_as(as[(j & 1) ^ 1], (j & 1) ^ 1);
+            __syncthreads();
+        }
     }
 
 #pragma unroll
