@@ -12,7 +12,7 @@
 // first -- and the lane's scale operand is the ue8m0 byte of that 32-block; the result
 // is C[4 q + i][t], i = 0..3, as for the bf16 16x16 MFMAs.
 //
-// Tiling as the bf16 grouped GEMM (row tiles MT = 4 or 8; the 16- and 32-row classes
+// Tiling as the bf16 grouped GEMM (row tiles MT = 4, 8 or 16; the 16- and 32-row classes
 // take the bf16 GEMM on exact bf16 copies of the quantized activations): a workgroup of 8
 // waves serves (item, column block), each wave two 16-column tiles (gate and up at the same
 // columns for the dual projection, two adjacent tiles of the down matrix otherwise) over
@@ -68,9 +68,9 @@ template <bool DUAL, int MT>
 __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int BM = 16 * MT;
     constexpr int STAGE = f4_stage_bytes(MT);
-    // steps of weights in flight (128 rows: three, faster than two or four) and the loop
-    // unroll, a multiple of NB and of 2
-    constexpr int NB = MT == 8 ? 3 : 2;
+    // steps of weights in flight (128 and 256 rows: three, faster than two or four) and
+    // the loop unroll, a multiple of NB and of 2
+    constexpr int NB = MT >= 8 ? 3 : 2;
     constexpr int UN = NB % 2 ? 2 * NB : NB;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     // left free, the compiler sank them below the loads and the barrier and held three
     // sets of weight registers (the 128-row form then spilled).
     auto pin_acc = [&] __attribute__((always_inline)) () {
-        if constexpr (MT == 8)
+        if constexpr (MT >= 8)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -322,6 +322,7 @@ hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *
     switch (mt) {                                                                             \
     case 4: return launch_f4_t<D_, 4>(a, n_items, st);                                        \
     case 8: return launch_f4_t<D_, 8>(a, n_items, st);                                        \
+    case 16: return launch_f4_t<D_, 16>(a, n_items, st);                                      \
     default: return hipErrorInvalidValue;                                                     \
     }
     if (dual) {

@@ -192,12 +192,14 @@ hipError_t launch_rmsnorm(const float *x, const float *w, float *y, int rows, in
 
 // Native MXFP4 GEMM (kern_fp4.hip): v_mfma_scale_f32_16x16x128_f8f6f4 with e2m1 activations
 // (codes [rcap][K/2] + ue8m0 scales [rcap][K/32], from launch_quantize_mxfp4) against the
-// MXFP4 weights as stored.  Items and workgroup tiling as launch_gemm (mt 4 and 8; an
+// MXFP4 weights as stored.  Items and workgroup tiling as launch_gemm (mt 4, 8 and 16; an
 // expert's row blocks run column block by column block);
 // the dual projection writes H = act(gate, up) as f32 [rcap][O], the single one Y.
 // Requires K % 256 == 0, O % 128 (dual) / % 256 (single) == 0, 16-byte aligned weights,
 // 8-byte aligned scales.
-constexpr int kFp4MaxMt = 8;
+constexpr int kFp4MaxMt = 16;
+// row classes of a grouped-GEMM call: 16, 32, 64, 128 and (native FP4 only) 256 rows
+constexpr int kGemmClasses = 5;
 // Row classes of a native-MXFP4 call (option fp4act) up to this one take the bf16 grouped
 // GEMM on bf16 copies of the quantized activations instead (launch_quantize_mxfp4's
 // planes): the same exact products, streamed faster (c4: gate/up 16-row class 794 ->

@@ -392,7 +392,7 @@ struct CallCfg {
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
-    GemmCls gcls[4];
+    GemmCls gcls[kGemmClasses];
     int n_gcls = 0;
 };
 
@@ -485,11 +485,11 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     // bf16 one-term GEMM: an expert of 33-64 rows (a last block of that size) runs as two
     // 32-row items of the two-workgroups-per-CU class, which read its weights together
     const bool split64 = !cc.f32 && !cc.fp4 && cc.terms == 1 && max_mt >= 4;
-    std::vector<int> per[4];  // class index = log2(mt)
-    size_t split_at[4] = {0, 0, 0, 0};
+    std::vector<int> per[kGemmClasses];  // class index = log2(mt)
+    size_t split_at[kGemmClasses] = {};
     for (size_t i = 0; i < P.ew.size(); ++i) {
         if (i == split)
-            for (int c = 0; c < 4; ++c)
+            for (int c = 0; c < kGemmClasses; ++c)
                 split_at[c] = per[c].size();
         const int n = P.ew[i].nrows;
         for (int r0 = 0; r0 < n; r0 += bm) {
@@ -499,18 +499,20 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
                                              static_cast<int>(i), r0 + 32, nrow - 32, 0});
                 continue;
             }
-            const int mt = nrow <= 16 ? 1 : nrow <= 32 ? 2 : nrow <= 64 ? 4 : 8;
-            const int c = mt == 1 ? 0 : mt == 2 ? 1 : mt == 4 ? 2 : 3;
+            int c = 0;  // smallest class of 16 * 2^c rows that holds the block
+            while ((16 << c) < nrow)
+                ++c;
             per[c].insert(per[c].end(), {static_cast<int>(i), r0, nrow, 0});
         }
     }
     if (split >= P.ew.size())
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < kGemmClasses; ++c)
             split_at[c] = per[c].size();
     // 4th word: (block index within the expert's run of items in this class) << 16 | run
-    // length; the scaled-FP4 kernel orders an expert's tasks column block by column block
-    // with these (runs of 2^15 blocks or more stay one item per run)
-    for (int c = 0; c < 4; ++c) {
+    // length; the scaled-FP4 kernels and the 16/32-row bf16 kernels order an expert's
+    // tasks column block by column block with these (runs of 2^15 blocks or more stay one
+    // item per run)
+    for (int c = 0; c < kGemmClasses; ++c) {
         std::vector<int> &v = per[c];
         for (size_t j = 0; j < v.size();) {
             size_t e = j;
@@ -524,7 +526,7 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     }
     cc.items.clear();
     cc.n_gcls = 0;
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kGemmClasses; ++c) {
         if (per[c].empty())
             continue;
         GemmCls &g = cc.gcls[cc.n_gcls++];

@@ -617,9 +617,9 @@ def test_prefill_config_parity(hip, orc, name, T):
 FP4_CASES = [
     # D, I, nr, S, act, a, b
     (1024, 512, [20, 5, 70, 1], 64, 2, 4.0, 25.0),    # bf16 classes 1/2, FP4 class 8
-    # an expert of three blocks (two 128-row FP4 items run column block by column block,
-    # then a 44-row one), a 64-row-class expert, the bf16 classes
-    (1024, 512, [300, 40, 20, 5], 160, 2, 4.0, 25.0),
+    # an expert of three blocks (two 256-row FP4 items run column block by column block,
+    # then an 88-row one), a 64-row-class expert, the bf16 classes
+    (1024, 512, [600, 40, 20, 5], 160, 2, 4.0, 25.0),
     (7168, 2048, [3, 40], 16, 2, 4.0, 25.0),           # K3 shapes
     (512, 256, [1, 1, 2], 3, 1, 7.0, 0.0),             # decode-shaped, clamped SwiGLU
 ]
