@@ -620,6 +620,9 @@ FP4_CASES = [
     # an expert of three blocks (two 256-row FP4 items run column block by column block,
     # then an 88-row one), a 64-row-class expert, the bf16 classes
     (1024, 512, [600, 40, 20, 5], 160, 2, 4.0, 25.0),
+    # K / 256 odd in the down projection (768 = 3 x 256): a row's 24 scale bytes end
+    # inside a 16-byte scale load, the last row's at the end of the buffer
+    (512, 768, [40, 90, 200], 96, 1, 7.0, 0.0),
     (7168, 2048, [3, 40], 16, 2, 4.0, 25.0),           # K3 shapes
     (512, 256, [1, 1, 2], 3, 1, 7.0, 0.0),             # decode-shaped, clamped SwiGLU
 ]
