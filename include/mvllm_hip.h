@@ -364,6 +364,10 @@ int mvllm_hip_tier_table_done(int layer, void *stream);
  *     including 16
  *  16 host ms of 15 spent blocked until the device finished earlier calls whose pinned
  *     plan slots are reused (a host running ahead of the device waits there)
+ *  17 (gauge) device bytes the HBM tier holds for blobs: resident plus parked; kept
+ *     within mvllm_hip_set_expert_budget
+ *  18 (gauge) of 17, the blocks of blobs dropped while their layer's tier tables are
+ *     open, held until mvllm_hip_tier_table_done recycles them
  * Kernel times are filled only with option "timing"=1.  Returns the count written
  * (<= n). */
 int mvllm_hip_stats(double *vals, int n);

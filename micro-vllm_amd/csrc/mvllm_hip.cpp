@@ -193,6 +193,7 @@ struct Ctx {
     // residency
     size_t budget = size_t(64) << 30;
     size_t used_bytes = 0;
+    size_t parked_bytes = 0;  // blocks of dropped blobs held until their layer's tables close
     std::unordered_map<long long, Resident> res;  // key = (layer << 32) | eid
     std::map<const uint8_t *, long long> by_host;  // host blob start -> key
     std::list<long long> lru;                      // front = most recent
@@ -214,7 +215,7 @@ struct Ctx {
     hipEvent_t tier_ready = nullptr;  // copy stream: every promotion enqueued so far
     std::vector<std::pair<size_t, void *>> pending_free;
     // stats
-    double stats[17] = {0};
+    double stats[19] = {0};
     std::vector<TimedCall> timed;
 };
 
@@ -1227,9 +1228,10 @@ void res_drop(Ctx &C, long long key) {
     if (lu != C.layer_use.end())
         (void)hipStreamWaitEvent(C.copy, lu->second, 0);
     auto lo = C.layer_open.find(r.layer);
-    if (lo != C.layer_open.end() && lo->second > 0)
+    if (lo != C.layer_open.end() && lo->second > 0) {
         C.layer_parked[r.layer].emplace_back(r.bytes, r.dev);
-    else
+        C.parked_bytes += r.bytes;  // still device memory of the tier: counted in the budget
+    } else
         C.free_blocks.emplace(r.bytes, r.dev);
     C.used_bytes -= r.bytes;
     if (r.host)
@@ -1313,6 +1315,7 @@ void mvllm_hip_shutdown(void) {
         for (auto &fb : lp.second)
             (void)hipFree(fb.second);
     C.layer_parked.clear();
+    C.parked_bytes = 0;
     C.layer_open.clear();
     C.H.release();
     C.Y.release();
@@ -1665,7 +1668,7 @@ int mvllm_hip_set_expert_budget(size_t bytes) {
     Ctx &C = ctx();
     std::lock_guard<std::mutex> lk(C.mu);
     C.budget = bytes;
-    while (C.used_bytes > C.budget && !C.lru.empty())
+    while (C.used_bytes + C.parked_bytes > C.budget && !C.lru.empty())
         res_drop(C, C.lru.back());
     return 1;
 }
@@ -1704,10 +1707,13 @@ int promote_locked(Ctx &C, const void *host_blob, size_t bytes, int layer, int e
             ++h;
         }
     }
-    while (C.used_bytes + bytes > C.budget && !C.lru.empty())
+    // parked blocks (blobs dropped while their layer's tables are open) count against the
+    // budget until mvllm_hip_tier_table_done recycles them
+    while (C.used_bytes + C.parked_bytes + bytes > C.budget && !C.lru.empty())
         res_drop(C, C.lru.back());
-    if (C.used_bytes + bytes > C.budget) {
-        set_err("promote: blob larger than the expert budget");
+    if (C.used_bytes + C.parked_bytes + bytes > C.budget) {
+        set_err(C.parked_bytes ? "promote: expert budget held by blobs of open tier tables"
+                               : "promote: blob larger than the expert budget");
         return 0;
     }
     void *dev = res_alloc(C, bytes);
@@ -1873,8 +1879,10 @@ int mvllm_hip_tier_table_done(int layer, void *stream) {
         // blobs of the layer dropped while its tables were open: copies into their
         // blocks wait for the readers recorded just now
         HIP_TRY(hipStreamWaitEvent(C.copy, ev, 0));
-        for (auto &fb : lp->second)
+        for (auto &fb : lp->second) {
             C.free_blocks.emplace(fb.first, fb.second);
+            C.parked_bytes -= fb.first;
+        }
         lp->second.clear();
     }
     return 1;
@@ -1916,7 +1924,9 @@ int mvllm_hip_stats(double *vals, int n) {
             (void)hipEventDestroy(e);
     }
     C.timed.clear();
-    const int m = std::min(n, 17);
+    C.stats[17] = static_cast<double>(C.used_bytes + C.parked_bytes);
+    C.stats[18] = static_cast<double>(C.parked_bytes);
+    const int m = std::min(n, 19);
     for (int i = 0; i < m; ++i)
         vals[i] = C.stats[i];
     return m;
@@ -2160,14 +2170,20 @@ int mvllm_hip_linear_dev(int fmt, const void *w, const void *scales, int O, int 
                              0.f, 0.f, st));
         return 1;
     }
-    // quantized: the input rows as two bf16 terms (2^-17 relative), then the grouped GEMM
+    // quantized: the input rows as two bf16 terms (2^-17 relative), then the grouped GEMM.
+    // The planes buffer is shared by every call: a call on another stream than the
+    // previous one waits for it first, as the block entry points do.
     ew.w[2] = w;
     ew.s[2] = scales;
     const int terms = 2;
     HIP_TRY(C.Lp.ensure((size_t)terms * 2 * n * K));
+    if (!order_after_previous(C, st))
+        return 0;
     HIP_TRY(launch_prep_planes(fmt, terms, x, nullptr, n, K, n, C.Lp.p, st));
     const int mt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
     HIP_TRY(launch_gemm_rows(fmt, terms, mt, &ew, n, C.Lp.p, y, K, O, st));
+    C.last_stream = st;
+    C.have_last = true;
     return 1;
 }
 

@@ -136,8 +136,8 @@ int stream_spans(const std::vector<StFileIdx> &files, const std::vector<Span> &s
 
 using namespace mvllm_hip;
 
-extern "C" long long mvllm_hip_slab_load(const char *dir, const char *prefix, int fmt, int D,
-                                         int I, int layer0, int layer1, int n_experts) {
+static long long slab_load_impl(const char *dir, const char *prefix, int fmt, int D, int I,
+                                int layer0, int layer1, int n_experts) {
     set_error("");
     if (!mvllm_hip_available()) {
         set_error("slab_load: mvllm_hip_init not called");
@@ -182,16 +182,26 @@ extern "C" long long mvllm_hip_slab_load(const char *dir, const char *prefix, in
             dst += p.bytes;
         }
     }
+    std::vector<const void *> table(n_blobs);
     hipError_t e = hipMalloc(&S.base, n_blobs * (size_t)S.stride);
     if (e == hipSuccess)
         e = hipMalloc(&S.table, n_blobs * sizeof(void *));
+    // the device blocks go back if anything below fails or throws
+    struct Guard {
+        Slab *s;
+        ~Guard() {
+            if (s) {
+                if (s->base)
+                    (void)hipFree(s->base);
+                if (s->table)
+                    (void)hipFree(s->table);
+            }
+        }
+    } guard{&S};
     if (e != hipSuccess) {
-        if (S.base)
-            (void)hipFree(S.base);
         set_error(std::string("slab_load: hipMalloc: ") + hipGetErrorString(e));
         return 0;
     }
-    std::vector<const void *> table(n_blobs);
     for (size_t b = 0; b < n_blobs; ++b)
         table[b] = static_cast<char *>(S.base) + b * (size_t)S.stride;
     if (!stream_spans(files, spans, static_cast<char *>(S.base)) ||
@@ -199,14 +209,26 @@ extern "C" long long mvllm_hip_slab_load(const char *dir, const char *prefix, in
                        hipMemcpyHostToDevice)) != hipSuccess) {
         if (e != hipSuccess)
             set_error(std::string("slab_load: hipMemcpy: ") + hipGetErrorString(e));
-        (void)hipFree(S.base);
-        (void)hipFree(S.table);
         return 0;
     }
     std::lock_guard<std::mutex> lk(g_mu);
     const long long h = g_next++;
     g_slabs[h] = S;
+    guard.s = nullptr;
     return h;
+}
+
+// C entry: no exception (allocation failure included) crosses the boundary
+extern "C" long long mvllm_hip_slab_load(const char *dir, const char *prefix, int fmt, int D,
+                                         int I, int layer0, int layer1, int n_experts) {
+    try {
+        return slab_load_impl(dir, prefix, fmt, D, I, layer0, layer1, n_experts);
+    } catch (const std::exception &x) {
+        set_error(std::string("slab_load: ") + x.what());
+    } catch (...) {
+        set_error("slab_load: unknown exception");
+    }
+    return 0;
 }
 
 extern "C" int mvllm_hip_slab_info(long long h, void **base, void **table, long long *stride,

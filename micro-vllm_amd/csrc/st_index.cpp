@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <cerrno>
+#include <climits>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -164,9 +165,19 @@ struct JReader {
                 ++p;
         }
         if (integral) {
-            if (p - s > 19)
-                return fail("integer out of range");
-            v = std::stoll(std::string(s, p));
+            // digits accumulated with an explicit bound: no library call that throws
+            const bool neg = *s == '-';
+            const unsigned long long lim =
+                neg ? (unsigned long long)LLONG_MAX + 1ull : (unsigned long long)LLONG_MAX;
+            unsigned long long a = 0;
+            for (const char *d = neg ? s + 1 : s; d < p; ++d) {
+                const unsigned dig = (unsigned)(*d - '0');
+                if (a > (lim - dig) / 10ull)
+                    return fail("integer out of range");
+                a = a * 10ull + dig;
+            }
+            v = neg ? (a == (unsigned long long)LLONG_MAX + 1ull ? LLONG_MIN : -(long long)a)
+                    : (long long)a;
         }
         return true;
     }
@@ -600,10 +611,11 @@ bool st_expert_pieces(const std::vector<StFileIdx> &files, const std::string &pr
 
 }  // namespace mvllm_hip
 
-extern "C" int mvllm_st_expert_pieces(const char *dir, const char *prefix, int fmt, int D, int I,
-                                      int layer0, int layer1, int n_experts, int *file,
-                                      long long *offset, long long *bytes, char *paths,
-                                      long long paths_cap, char *err, long long err_cap) {
+namespace {
+int expert_pieces_impl(const char *dir, const char *prefix, int fmt, int D, int I, int layer0,
+                       int layer1, int n_experts, int *file, long long *offset,
+                       long long *bytes, char *paths, long long paths_cap, char *err,
+                       long long err_cap) {
     using namespace mvllm_hip;
     std::string e;
     std::vector<StFileIdx> files;
@@ -645,4 +657,23 @@ extern "C" int mvllm_st_expert_pieces(const char *dir, const char *prefix, int f
     }
     put_err("");
     return (int)files.size();
+}
+}  // namespace
+
+// C entry: no exception (allocation failure included) crosses the boundary
+extern "C" int mvllm_st_expert_pieces(const char *dir, const char *prefix, int fmt, int D, int I,
+                                      int layer0, int layer1, int n_experts, int *file,
+                                      long long *offset, long long *bytes, char *paths,
+                                      long long paths_cap, char *err, long long err_cap) {
+    try {
+        return expert_pieces_impl(dir, prefix, fmt, D, I, layer0, layer1, n_experts, file,
+                                  offset, bytes, paths, paths_cap, err, err_cap);
+    } catch (const std::exception &x) {
+        if (err && err_cap > 0)
+            std::snprintf(err, (size_t)err_cap, "st_expert_pieces: %s", x.what());
+    } catch (...) {
+        if (err && err_cap > 0)
+            std::snprintf(err, (size_t)err_cap, "st_expert_pieces: unknown exception");
+    }
+    return -1;
 }

@@ -315,6 +315,26 @@ int host_checks(int iters, uint32_t seed) {
         std::fprintf(stderr, "good container refused: %s\n", err);
         ++failures;
     }
+    // offsets of 19 and 20 digits past the 64-bit range: an error, not an exception
+    for (const char *big : {"9999999999999999999", "18446744073709551616",
+                            "-9223372036854775809"}) {
+        std::string h = header;
+        const size_t at = h.find("\"data_offsets\":[0,");
+        const size_t e = h.find(']', at);
+        h.replace(at, e - at, std::string("\"data_offsets\":[0,") + big);
+        std::string b;
+        put_le64(b, h.size());
+        b += h;
+        b += good.substr(8 + header.size());
+        write(b);
+        err[0] = '\0';
+        if (mvllm_st_expert_pieces(dir, "", 7, 32, 32, 0, 1, 1, file, off, by, nullptr, 0, err,
+                                   sizeof(err)) != -1 ||
+            !std::strstr(err, "out of range")) {
+            std::fprintf(stderr, "offset %s: not refused as out of range (%s)\n", big, err);
+            ++failures;
+        }
+    }
     // mutated containers: byte flips in the header, truncations, bad lengths; each must
     // give an answer (pieces or an error), never a crash
     uint32_t s = 12345 + seed;
@@ -392,11 +412,11 @@ int main(int argc, char **argv) {
         for (int t = 0; t < 4; ++t)
             th.emplace_back([&, t] { bad += host_checks(iters, 1000u * (uint32_t)(t + 1)); });
         th.emplace_back([&] {
-            double sv[17];
+            double sv[19];
             for (int i = 0; i < iters; ++i) {
                 mvllm_hip_set_option("combine_ordered", i & 1);
                 mvllm_hip_set_option("mode", i % 3);
-                mvllm_hip_stats(sv, 17);
+                mvllm_hip_stats(sv, 19);
                 if (i % 7 == 0)
                     mvllm_hip_stats_reset();
                 // refused without a device; the error text is per thread
@@ -421,7 +441,8 @@ int main(int argc, char **argv) {
     }
     g_blob = mvllm_expert_geom(kFmt, kD, kI, g_off);
     // HBM budget for about two layers' worth of a call's experts: promotions evict
-    mvllm_hip_set_expert_budget((size_t)g_blob * 2 * kSlotsPerLayer);
+    const size_t budget = (size_t)g_blob * 2 * kSlotsPerLayer;
+    mvllm_hip_set_expert_budget(budget);
     RamTier ram;
     if (!ram.open()) {
         std::fprintf(stderr, "host_alloc failed\n");
@@ -549,6 +570,16 @@ int main(int argc, char **argv) {
                 reinterpret_cast<int *>(s + 512), reinterpret_cast<int *>(s + 768), kExperts,
                 reinterpret_cast<int *>(s + 1024), reinterpret_cast<float *>(s + 2048),
                 kTok * kTopk, dx, dout, kTok, 2, 4.f, 25.f, nullptr, st);
+            {
+                // the table is still open here while the store thread promotes: the tier's
+                // device memory (resident plus parked blocks) stays within the budget
+                double sv[19];
+                if (mvllm_hip_stats(sv, 19) == 19 && sv[17] > (double)budget) {
+                    std::fprintf(stderr, "step %d layer %d: tier holds %.0f bytes, budget %zu\n",
+                                 step, layer, sv[17], budget);
+                    failures++;
+                }
+            }
             mvllm_hip_tier_table_done(layer, st);
             std::vector<float> out2((size_t)kTok * kD);
             (void)hipMemcpyAsync(out2.data(), dout, out2.size() * 4, hipMemcpyDeviceToHost, st);

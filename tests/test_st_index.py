@@ -131,7 +131,8 @@ def test_glm_float_codes_refused(tmp_path):
 
 
 @pytest.mark.parametrize("case", ["zero_header", "huge_header", "not_object", "bad_json",
-                                  "inverted", "no_dtype", "past_end", "no_dir"])
+                                  "inverted", "no_dtype", "past_end", "no_dir",
+                                  "huge_offset", "max_offset", "min_offset"])
 def test_malformed_containers(tmp_path, case):
     fmt, D, I = 7, 32, 32
     nbytes = piece_bytes(fmt, D, I)
@@ -146,7 +147,9 @@ def test_malformed_containers(tmp_path, case):
               "huge_header": "invalid safetensors header_size",
               "not_object": "not an object", "bad_json": "safetensors header",
               "inverted": "data_offsets inverted", "no_dtype": "missing dtype",
-              "past_end": "past the end", "no_dir": "opendir"}[case]
+              "past_end": "past the end", "no_dir": "opendir",
+              "huge_offset": "integer out of range", "max_offset": "wrong size",
+              "min_offset": "data_offsets"}[case]
     if case == "zero_header":
         raw = struct.pack("<Q", 0) + raw[8:]
     elif case == "huge_header":
@@ -170,6 +173,17 @@ def test_malformed_containers(tmp_path, case):
         raw = struct.pack("<Q", len(h)) + h + raw[8 + n:]
     elif case == "past_end":
         raw = raw[:-10]
+    elif case in ("huge_offset", "max_offset", "min_offset"):
+        # 19- and 20-digit offsets: out of the 64-bit range must be an error, not an
+        # exception escaping the C entry point
+        big = {"huge_offset": "9999999999999999999", "max_offset": "9223372036854775807",
+               "min_offset": "-9223372036854775808"}[case]
+        d = json.loads(header)
+        k = next(iter(d))
+        lo, hi = d[k]["data_offsets"]
+        h = json.dumps(d).replace(f"[{lo}, {hi}]", f"[{lo}, {big}]" if case != "min_offset"
+                                  else f"[{big}, {hi}]", 1).encode()
+        raw = struct.pack("<Q", len(h)) + h + raw[8 + n:]
     path.write_bytes(raw)
     where = str(tmp_path / "absent") if case == "no_dir" else str(tmp_path)
     with pytest.raises(hip.HipError, match=expect):
