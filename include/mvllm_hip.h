@@ -120,9 +120,13 @@ int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
  *   "fp4act" 1 = MXFP4 experts (fmt 7) run on native MXFP4 activations: the GEMM inputs
  *            (x, then h) are quantized exactly as fp4_activation_qdq with block 32
  *            (src/quant/native_act.cpp:159-179) and fed with the weights as stored to the
- *            scaled FP4 matrix cores.  Changes the numbers (activation quantization);
- *            weight scale bytes 0 and 255 act as the hardware's 2^-127 and NaN, not the
- *            reference's +0 and +inf.
+ *            scaled FP4 matrix cores.  Changes the numbers (activation quantization).
+ *            Weight scale bytes 0 and 255 keep the reference's +0 and +inf: a wave of the
+ *            scaled-FP4 kernel that meets one computes its outputs element by element.
+ *   "gemm_wide" 1 (default) = the 128-row blocks of MXFP4 experts in the one-term grouped
+ *            GEMM run a kernel with wide wave tiles (8 waves of 128 rows x 64 weight
+ *            columns), 2 = 4 waves of 128 x 128, 0 = the grouped GEMM's own 128-row
+ *            class.  Same products; sums in another order.
  *   "combine_ordered" 1 = decode calls of mvllm_hip_moe_block_dev also run the separate
  *            combine kernel, which applies out[t] += w * y in the reference's expert order
  *            (bit-exact given the same expert outputs); by default they fold the combine

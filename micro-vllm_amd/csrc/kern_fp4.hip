@@ -230,6 +230,10 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     F4Step b[NB];
     F4Scl sc, sn;  // scale chunk of this step / the next chunk
     u32x2 as[2];
+    // Weight scale bytes the matrix cores read differently from the reference (0 and 255,
+    // ue8m0_special), noted as each chunk opens: a wave that met one recomputes its
+    // outputs element by element instead (below).
+    uint32_t exc = 0;
     dma_a(0, 0);
     as[0] = load_as(0);
     load_b(b[0], 0);
@@ -246,8 +250,14 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             const int kk = k + j;
             if (j > 0 && kk >= nk)
                 break;
-            if (j % 2 == 0 && (kk & 7) == 0)
+            if (j % 2 == 0 && (kk & 7) == 0) {
                 sc = sn;
+                // this lane's 16 bytes of the chunk that lie in its row
+                const int valid = (int)srow - 64 * (kk >> 3) - 16 * q;
+#pragma unroll
+                for (int m = 0; m < 2; ++m)
+                    exc |= ue8m0_special(sc.c[m], valid);
+            }
             dma_a(min(kk + 1, nk - 1), (j & 1) ^ 1);
             as[j & 1] = load_as(min(kk + 2, nk - 1));
             if (j & 1)
@@ -262,6 +272,64 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
             store_as(as[(j & 1) ^ 1], (j & 1) ^ 1);
             __syncthreads();
         }
+    }
+
+    // Rare: a weight scale byte 0 or 255 among the wave's columns.  The wave computes its
+    // outputs again element by element, as the composed reference does: x * (lut[n] *
+    // scale) with the reference's scales (+0, +inf), products exact in f32, summed in K
+    // order, so +-inf and NaN land where the reference puts them.  No barrier: the wave
+    // reads the activation codes and the weights from memory.
+    if (__builtin_amdgcn_ballot_w64(exc != 0) != 0) {
+        const uint8_t *wc[2], *ws[2];
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+            const int mi = DUAL ? m : 2;
+            const size_t wrow = (size_t)((DUAL ? col0 : col0 + 16 * m) + t);
+            wc[m] = static_cast<const uint8_t *>(ew.w[mi]) + wrow * rowb;
+            ws[m] = static_cast<const uint8_t *>(ew.s[mi]) + wrow * srow;
+        }
+        for (int mt = 0; mt < MT; ++mt) {
+            float sum[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            for (int blk = 0; blk < (int)srow; ++blk) {
+                u32x4 wv[2];
+                float wsc[2];
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    wv[m] = *reinterpret_cast<const u32x4 *>(wc[m] + 16 * blk);
+                    wsc[m] = ue8m0_ref(ws[m][blk]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = min(mt * 16 + 4 * q + i, nrow - 1);
+                    const u32x4 av = *reinterpret_cast<const u32x4 *>(
+                        A.acode + (size_t)(jbase + r) * rowb + 16 * blk);
+                    const float asc = ue8m0_ref(A.ascale[(size_t)(jbase + r) * srow + blk]);
+                    for (int e = 0; e < 32; ++e) {
+                        const float x = e2m1_val((av[e >> 3] >> (4 * (e & 7))) & 15u) * asc;
+#pragma unroll
+                        for (int m = 0; m < 2; ++m) {
+                            const float w =
+                                e2m1_val((wv[m][e >> 3] >> (4 * (e & 7))) & 15u) * wsc[m];
+                            sum[m][i] += x * w;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = mt * 16 + 4 * q + i;
+                if (r >= nrow)
+                    continue;
+                const size_t j = (size_t)(jbase + r);
+                if constexpr (DUAL) {
+                    A.hout[j * O + col0 + t] = mf_act(A.act, sum[0][i], sum[1][i], A.act_a, A.act_b);
+                } else {
+                    A.out[j * O + col0 + t] = sum[0][i];
+                    A.out[j * O + col0 + 16 + t] = sum[1][i];
+                }
+            }
+        }
+        return;
     }
 
 #pragma unroll

@@ -116,6 +116,40 @@ __device__ __forceinline__ bool b7_exceptional(float scale7) {
     return e < 2u || e > 252u;
 }
 
+// ---- MXFP4 weight scale bytes the scaled matrix cores read differently --------------
+// The matrix cores read an ue8m0 byte e as 2^(e-127) for 0..254 and 255 as NaN; the
+// reference's mx4_scale gives +0 for e = 0 and +inf for e = 255 (src/quant/quant.hpp:12-20).
+// Every other byte agrees.
+
+// Bits of the first `valid` bytes of a 16-byte chunk of scale bytes: 1 = some byte is 0 or
+// 255, 2 = some byte is 255 (bytes past `valid` belong to another row or lie past the
+// buffer and are ignored).
+__device__ __forceinline__ uint32_t ue8m0_special(u32x4 c, int valid) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int nv = min(max(valid - 4 * i, 0), 4);
+        const uint32_t keep = nv >= 4 ? 0xffffffffu : (1u << (8 * nv)) - 1u;
+        const uint32_t v = (c[i] & keep) | (0x7f7f7f7fu & ~keep);  // ignored bytes: 127
+        const uint32_t nz = ~v;                                     // bytes 255 -> 0
+        const uint32_t zero = (v - 0x01010101u) & ~v & 0x80808080u;
+        const uint32_t full = (nz - 0x01010101u) & ~nz & 0x80808080u;
+        r |= (zero | full) ? 1u : 0u;
+        r |= full ? 2u : 0u;
+    }
+    return r;
+}
+
+// e2m1 code n -> its value (the reference's mx4_lut: code 8 is -0).
+__device__ __forceinline__ float e2m1_val(uint32_t n) {
+    const uint32_t e = (n >> 1) & 3u, m = n & 1u;
+    const float mag = e == 0 ? 0.5f * (float)m : (1.f + 0.5f * (float)m) * (float)(1u << (e - 1));
+    return (n & 8u) ? -mag : mag;
+}
+
+// ue8m0 byte -> the reference's scale bits(e << 23): e = 0 is +0, e = 255 is +inf.
+__device__ __forceinline__ float ue8m0_ref(uint32_t e) { return __uint_as_float(e << 23); }
+
 // Position of K element e (within its 8-block) in the stored A row.
 template <int FMT>
 __device__ __forceinline__ int a_slot(int e) {

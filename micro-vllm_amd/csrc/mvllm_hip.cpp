@@ -390,6 +390,7 @@ struct CallCfg {
     bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
     bool f32 = false;         // fmt 0: the f32 matrix-core GEMM (kern_f32.hip)
     bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
+    bool w16 = false;         // every weight pointer 16-byte aligned (the wide-tile GEMM)
     int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
     PhaseCfg gu, dn;
     std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
@@ -566,8 +567,11 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
     }
     const size_t walign = fmt == 7 && C.fp4act ? 16 : 8;  // the FP4 GEMM loads 16-byte rows
     int most = 0;
+    bool w16 = true;
     for (const ExpertWork &w : P.ew) {
         most = std::max(most, w.nrows);
+        for (int m = 0; m < 3; ++m)
+            w16 = w16 && aligned(w.w[m], 16);
         for (int m = 0; m < 3; ++m) {
             ok = ok && aligned(w.w[m], 16) && aligned(w.s[m], fmt == 4 ? 16 : 8);
             gok = gok && aligned(w.w[m], walign) && aligned(w.s[m], fmt == 4 ? 16 : 8);
@@ -583,6 +587,7 @@ void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, 
     if (gok && C.gemm != 2 && (C.gemm == 1 || most > 16)) {
         cc.terms = C.mode == 1 ? 2 : 1;
         plan_gemm(cc, P, split, fmt);
+        cc.w16 = w16;
         return;
     }
     if (ok && pick_rmax(fmt, D, I, cc.terms, true, 1) >= 1 &&
@@ -896,6 +901,19 @@ int finish_call(Ctx &C, hipStream_t st, int si) {
     return 1;
 }
 
+// One row class of the grouped GEMM: the 128-row blocks of MXFP4 experts in one-term
+// bf16 arithmetic take the wide-tile kernel when the shapes and alignment allow.
+hipError_t launch_gemm_cls(bool w16, int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
+                           const void *items, int n_items, const void *pin, void *pout,
+                           float *out, int K, int O, int rcap, int act, float act_a, float act_b,
+                           hipStream_t st, const int *n_items_dev = nullptr) {
+    if (w16 && fmt == 7 && terms == 1 && mt == 8 && gemm_wide_fits(dual, K, O))
+        return launch_gemm_wide(dual, ew, items, n_items, pin, pout, out, K, O, rcap, act, act_a,
+                                act_b, st, n_items_dev);
+    return launch_gemm(fmt, dual, terms, mt, ew, items, n_items, pin, pout, out, K, O, rcap, act,
+                       act_a, act_b, st, n_items_dev);
+}
+
 GemvArgs generic_args(const DevPlan &dp, size_t first, size_t count, const int *in_rows,
                       const float *in, float *out, int K, int O, int act, float a, float b) {
     GemvArgs g{};
@@ -1022,9 +1040,9 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
                 const size_t i0 = part ? g.it_split : g.it0, i1 = part ? g.it1 : g.it_split;
                 if (i1 <= i0)
                     continue;
-                HIP_TRY(launch_gemm(fmt, true, cc.terms, g.mt, dp.ew, dp.items + 4 * i0,
-                                    static_cast<int>(i1 - i0), B.Xp, B.Ph, nullptr, D, I,
-                                    rcap, act, a, b, st));
+                HIP_TRY(launch_gemm_cls(cc.w16, fmt, true, cc.terms, g.mt, dp.ew,
+                                        dp.items + 4 * i0, static_cast<int>(i1 - i0), B.Xp, B.Ph,
+                                        nullptr, D, I, rcap, act, a, b, st));
                 C.stats[13] += 1;
             }
         }
@@ -1032,9 +1050,10 @@ int run_phases(Ctx &C, const Plan &P, const CallCfg &cc, const DevPlan &dp, cons
         HIP_TRY(mark(3));
         for (int c = 0; c < cc.n_gcls; ++c) {
             const GemmCls &g = cc.gcls[c];
-            HIP_TRY(launch_gemm(fmt, false, cc.terms, g.mt, dp.ew, dp.items + 4 * g.it0,
-                                static_cast<int>(g.it1 - g.it0), B.Ph, nullptr,
-                                static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f, st));
+            HIP_TRY(launch_gemm_cls(cc.w16, fmt, false, cc.terms, g.mt, dp.ew,
+                                    dp.items + 4 * g.it0, static_cast<int>(g.it1 - g.it0), B.Ph,
+                                    nullptr, static_cast<float *>(B.Y), I, D, rcap, 0, 0.f, 0.f,
+                                    st));
             C.stats[14] += 1;
         }
     } else if (cc.mfma) {
@@ -1393,6 +1412,10 @@ int mvllm_hip_set_option(const char *key, long long value) {
         C.dec_ks = static_cast<int>(value);
     } else if (k == "gemm_xcd") {
         gemm_set_xcd(value != 0);
+    } else if (k == "gemm_wide") {
+        if (value < 0 || value > 2)
+            return 0;
+        gemm_set_wide(static_cast<int>(value));
     } else if (k == "dec_inline") {
         C.dec_inline = value ? 1 : 0;
     } else if (k == "combine_ordered") {
@@ -2095,16 +2118,21 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     HIP_TRY(launch_dplan(a, st));
     HIP_TRY(launch_prep_planes(fmt, terms, x, rows, cap_rows, D, cap_rows, C.Xp.p, st,
                                counts + 1, S));
+    // blobs are 256-byte aligned (k_dplan skips others): the pieces are 16-byte aligned
+    // when their offsets are
+    bool w16 = true;
+    for (int k = 0; k < 6; k += 2)
+        w16 = w16 && off6[k] % 16 == 0;
     for (int c = 0; c <= top; ++c)
         if (cap[c])
-            HIP_TRY(launch_gemm(fmt, true, terms, 1 << c, a.ew, a.items + base[c], cap[c], C.Xp.p,
-                                C.Ph.p, nullptr, D, Iinter, cap_rows, act, act_a, act_b, st,
-                                a.n_items + c));
+            HIP_TRY(launch_gemm_cls(w16, fmt, true, terms, 1 << c, a.ew, a.items + base[c], cap[c],
+                                    C.Xp.p, C.Ph.p, nullptr, D, Iinter, cap_rows, act, act_a,
+                                    act_b, st, a.n_items + c));
     for (int c = 0; c <= top; ++c)
         if (cap[c])
-            HIP_TRY(launch_gemm(fmt, false, terms, 1 << c, a.ew, a.items + base[c], cap[c],
-                                C.Ph.p, nullptr, static_cast<float *>(C.Y.p), Iinter, D,
-                                cap_rows, 0, 0.f, 0.f, st, a.n_items + c));
+            HIP_TRY(launch_gemm_cls(w16, fmt, false, terms, 1 << c, a.ew, a.items + base[c],
+                                    cap[c], C.Ph.p, nullptr, static_cast<float *>(C.Y.p), Iinter,
+                                    D, cap_rows, 0, 0.f, 0.f, st, a.n_items + c));
     HIP_TRY(launch_dcsr(cs, st));
     CombineArgs cb{};
     cb.Y = static_cast<const float *>(C.Y.p);

@@ -550,9 +550,6 @@ int main(int argc, char **argv) {
                 std::fprintf(stderr, "tier_table: %s\n", mvllm_hip_last_error());
                 failures++;
             }
-            int all = 1;
-            for (int i = 0; i < c.nb; ++i)
-                all &= mvllm_hip_resident_ptr(layer, c.eids[i]) != nullptr;
             // segments into device memory: counts, eids, xoff, nr, rows, rw
             char *s = static_cast<char *>(dsegs);
             int counts[2] = {c.nb, c.n_rows};
@@ -582,8 +579,16 @@ int main(int argc, char **argv) {
             }
             mvllm_hip_tier_table_done(layer, st);
             std::vector<float> out2((size_t)kTok * kD);
+            std::vector<void *> seen(kExperts);
             (void)hipMemcpyAsync(out2.data(), dout, out2.size() * 4, hipMemcpyDeviceToHost, st);
+            (void)hipMemcpyAsync(seen.data(), table, kExperts * sizeof(void *),
+                                 hipMemcpyDeviceToHost, st);
             (void)hipStreamSynchronize(st);
+            // the call's experts all in the table the routed call read (the store thread
+            // promotes and evicts meanwhile, so residency is read from that table itself)
+            int all = 1;
+            for (int i = 0; i < c.nb; ++i)
+                all &= seen[c.eids[i]] != nullptr;
             if (!ok) {
                 std::fprintf(stderr, "routed: %s\n", mvllm_hip_last_error());
                 failures++;

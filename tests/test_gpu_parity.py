@@ -676,6 +676,44 @@ def test_fp4act_config_c4(hip, orc):
     _fp4_check(got, exp)
 
 
+@pytest.mark.parametrize("act,a,b", [(2, 4.0, 25.0), (1, 7.0, 0.0)])
+def test_fp4act_special_scale_bytes(hip, orc, act, a, b):
+    """Weight scale bytes 0, 1, 254 and 255 in gate, up and down under fp4act, in every
+    row class (bf16 16/32-row classes; scaled-FP4 64-, 128- and 256-row blocks).  The
+    matrix cores read byte 0 as 2^-127 and 255 as NaN where the reference's mx4_scale gives
+    +0 and +inf (src/quant/quant.hpp:12-20): NaN and +-inf must land where the composed
+    oracle puts them, and the finite part must meet the fp4act bar."""
+    say("fp4act special scale bytes", act)
+    rng = np.random.default_rng(4242 + act)
+    # 70 rows: 128-row FP4 class; 40: 64-row; 300: a 256-row block + a 44-row one;
+    # 20: bf16 32-row class; 130: 256-row class
+    nr = [70, 40, 300, 20, 130]
+    c = random_case(rng, 7, 512, 256, nr, 600, act, a, b)
+    c.gs[0][5, 2] = 255
+    c.us[0][9, 3] = 0
+    c.ds[1][7, 1] = 255
+    c.ds[1][100, 0] = 0
+    c.gs[2][200, 15] = 255   # the last byte of its row
+    c.us[2][3, 0] = 1
+    c.ds[2][511, 7] = 255    # the last byte of the buffer
+    c.gs[3][9, 4] = 254
+    c.ds[3][3, 3] = 255
+    c.ds[4][50, 2] = 0
+    c.gs[4][77, 6] = 1
+    c.us[4][30, 1] = 255
+    got = _fp4_run(hip, c)
+    exp = c.out.copy()
+    assert orc.moe_block_fp4act(*c.args(exp), act, a, b) == 1
+    n_nan, n_inf = int(np.isnan(exp).sum()), int(np.isinf(exp).sum())
+    say("  oracle: nan", n_nan, "inf", n_inf)
+    assert n_nan + n_inf > 0
+    assert np.array_equal(np.isnan(got), np.isnan(exp))
+    assert np.array_equal(np.isinf(got), np.isinf(exp))
+    assert np.array_equal(np.sign(got[np.isinf(exp)]), np.sign(exp[np.isinf(exp)]))
+    fin = np.isfinite(exp)
+    _fp4_check(got[fin], exp[fin])
+
+
 @pytest.mark.parametrize("case", [DEV_CASES[1], DEV_CASES[3], DEV_CASES[7], DEV_CASES[-2]])
 def test_combine_ordered_vs_atomic(hip, orc, case):
     """Decode calls fold the combine into the down kernel (float atomics, any order);

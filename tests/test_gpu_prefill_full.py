@@ -36,7 +36,9 @@ def say(*a):
 
 def sample_rows(nr, xoff, rng):
     """(expert index, rows of that expert) triples: the heaviest expert across all its
-    128-row blocks, a mid-size expert, and the tail (one row of each of the smallest)."""
+    128-row blocks, a mid-size expert, one expert of each size range that a row class of
+    its own serves (33-64, 65-128, 129-256 and more rows), and the tail (one row of each of
+    the smallest)."""
     order = np.argsort(-nr, kind="stable")
     heavy = int(order[0])
     n_h = int(nr[heavy])
@@ -45,6 +47,15 @@ def sample_rows(nr, xoff, rng):
     mid = int(order[len(order) // 8])
     n_m = int(nr[mid])
     picks[mid] = sorted(rng.choice(n_m, size=min(N_SAMPLE, n_m), replace=False).tolist())
+    for lo, hi in ((33, 64), (65, 128), (129, 256), (257, 1 << 30)):
+        for e in order:
+            e = int(e)
+            if lo <= int(nr[e]) <= hi and e not in picks:
+                n_e = int(nr[e])
+                # its first and last rows, and rows between
+                picks[e] = sorted(set([0, n_e - 1] + rng.choice(
+                    n_e, size=min(N_SAMPLE // 2, n_e), replace=False).tolist()))
+                break
     for e in order[::-1][:N_SAMPLE]:
         e = int(e)
         if e not in picks:
@@ -124,13 +135,16 @@ def test_prefill_full_size(hip, orc, name, T):
 
 
 def test_prefill_full_size_fp4act(hip, orc):
-    """c4 at its full size with native MXFP4 activations (option fp4act): the heavy experts
-    through the scaled-FP4 kernel in 64-row blocks, the 16/32-row classes through the bf16
-    GEMM on exact bf16 copies of the quantized activations.  Sampled rows (as above) against
-    the composed oracle (fp4_activation_qdq on x and H around the f32 moe_block maths,
-    nb = 1 on those rows), with the native-FP4 bar: products are exact, so only the
-    summation order differs, except where it moves an h value across an e2m1 rounding
-    boundary (rare; one code step of one h element)."""
+    """c4 at its full size with native MXFP4 activations (option fp4act): experts of more
+    than 32 rows through the scaled-FP4 kernel in 256-row blocks, each remainder in the
+    smallest of the 64-, 128- and 256-row classes that holds it; the 16/32-row classes
+    through the bf16 GEMM on exact bf16 copies of the quantized activations.  Sampled rows
+    (as above, an expert of each class among them) against the composed oracle
+    (fp4_activation_qdq on x and H around the f32 moe_block maths, nb = 1 on those rows),
+    with the native-FP4 bar per row (each row's error over its own largest |ref|) and
+    over all rows: products are exact, so only the summation order differs, except where
+    it moves an h value across an e2m1 rounding boundary (rare; one code step of one h
+    element)."""
     from mvllm_hip import synth
     name, T = "c4", 2048
     say("prefill full size fp4act", name, T)
@@ -170,7 +184,12 @@ def test_prefill_full_size_fp4act(hip, orc):
     got, exp = np.concatenate(gots), np.concatenate(exps)
     den = np.max(np.abs(exp))
     dev_ = np.abs(got.astype(np.float64) - exp) / den
+    # per row: over the row's own largest |ref| (floored at 1e-3 of the global one, for a
+    # row whose reference is all but zero)
+    den_r = np.maximum(np.max(np.abs(exp), axis=1, keepdims=True), 1e-3 * den)
+    row_err = np.max(np.abs(got.astype(np.float64) - exp) / den_r, axis=1)
     say(f"  {got.shape[0]} rows of {len(picks)} experts: rel_err max {float(dev_.max()):.2e}, "
-        f"p99 {float(np.quantile(dev_, 0.99)):.2e}")
+        f"p99 {float(np.quantile(dev_, 0.99)):.2e}, worst row {float(row_err.max()):.2e}")
+    assert float(row_err.max()) < TOL_ROW
     assert float(dev_.max()) < 1e-2
     assert float(np.quantile(dev_, 0.99)) < 1e-5

@@ -4,7 +4,9 @@ assembly and reads each kernel's resource descriptor).
 The grouped GEMM's speed depends on its row classes fitting their VGPR budgets: a
 change that adds live registers makes the compiler spill to scratch memory, which cost
 ~15 % per call when it happened.  The bars are the spill bytes of the kept build: none
-for the 16- and 64-row classes, the FP4 and f32 GEMMs; at most 32 bytes elsewhere.
+for the 16- and 64-row classes, the FP4, f32 and wide-tile GEMMs (the eight-wave form, the
+default; each of its waves must stay within 256 VGPRs, two waves per SIMD); at most 32
+bytes elsewhere.
 """
 import os
 import re
@@ -56,11 +58,14 @@ def test_gemm_classes_within_register_budget(tmp_path):
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 @pytest.mark.parametrize("src,kernel", [("kern_fp4.hip", "k_gemm_fp4"),
-                                        ("kern_f32.hip", "k_f32mm")])
+                                        ("kern_f32.hip", "k_f32mm"),
+                                        ("kern_wide.hip", "k_gemm_wide<true, 8, 4, 8>"),
+                                        ("kern_wide.hip", "k_gemm_wide<false, 8, 4, 8>")])
 def test_other_gemms_spill_free(tmp_path, src, kernel):
     res = kernel_resources(os.path.join(CSRC, src), tmp_path)
     names = demangle(list(res))
     hits = [(names[k], v) for k, v in res.items() if kernel in names[k]]
     assert hits
-    for name, (scratch, _) in hits:
+    for name, (scratch, vgpr) in hits:
         assert scratch == 0, f"{name}: {scratch} bytes of scratch"
+        assert vgpr <= 256, f"{name}: {vgpr} VGPRs"
