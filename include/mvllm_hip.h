@@ -125,8 +125,8 @@ int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
  *            scaled-FP4 kernel that meets one computes its outputs element by element.
  *   "gemm_wide" 1 (default) = the 128-row blocks of MXFP4 experts in the one-term grouped
  *            GEMM run a kernel with wide wave tiles (8 waves of 128 rows x 64 weight
- *            columns), 2 = 4 waves of 128 x 128, 0 = the grouped GEMM's own 128-row
- *            class.  Same products; sums in another order.
+ *            columns), 0 = the grouped GEMM's own 128-row class.  Same products; sums in
+ *            another order.
  *   "combine_ordered" 1 = decode calls of mvllm_hip_moe_block_dev also run the separate
  *            combine kernel, which applies out[t] += w * y in the reference's expert order
  *            (bit-exact given the same expert outputs); by default they fold the combine

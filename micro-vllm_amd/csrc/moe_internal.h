@@ -164,7 +164,7 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
                        int K, int O, int rcap, int act, float act_a, float act_b,
                        hipStream_t st, const int *n_items_dev = nullptr);
 // The 128-row class of MXFP4 weights with one bf16 term (kern_wide.hip): wide wave tiles
-// (option "gemm_wide": 1 = eight waves of 128 rows x 4 tiles, 2 = four of 128 x 8, 0 = the
+// (option "gemm_wide": 1 = eight waves of 128 rows x 4 tiles of 16 weight rows, 0 = the
 // grouped GEMM above).  Same items, planes and outputs as launch_gemm at mt 8; requires
 // K % 256 == 0 and O % 256 (dual) / % 512 (single) == 0 (gemm_wide_fits), 16-byte aligned
 // weights.  launch_gemm takes this path itself when it fits.

@@ -1413,9 +1413,10 @@ int mvllm_hip_set_option(const char *key, long long value) {
     } else if (k == "gemm_xcd") {
         gemm_set_xcd(value != 0);
     } else if (k == "gemm_wide") {
-        if (value < 0 || value > 2)
+        if (value < 0 || value > 1)
             return 0;
         gemm_set_wide(static_cast<int>(value));
+
     } else if (k == "dec_inline") {
         C.dec_inline = value ? 1 : 0;
     } else if (k == "combine_ordered") {
