@@ -293,6 +293,10 @@ def main():
     sizes = probe_sizes(np, mvllm_hip, pool.pool, sink, probe_bytes) if args.probe_sizes else {}
 
     extra = {}
+    if args.config == "c4":
+        hot = hot_segments(np, torch, mvllm_hip, w, pool, cfg, T, args.steps, 2)
+        if hot:
+            extra["c4 hot segments"] = hot
     if not args.no_extra:
         if args.config == "c4" and not args.fp4act:
             rec, _, _ = measure(np, torch, mvllm_hip, synth, "c4", T, args.steps, 2,
@@ -341,6 +345,65 @@ def main():
         "extra": extra,
     }
     print(json.dumps(rec), flush=True)
+
+
+def hot_segments(np, torch, mvllm_hip, w, pool, cfg, T, steps, warmup, min_rows=332):
+    """Matrix-core utilisation of the compute-bound segments: the experts of the workload
+    with >= min_rows rows (at c4, the experts that are compute-bound even on the FP4 peak),
+    as one moe_block_dev call over those experts only (their rows, combine weights and out
+    rows as in the full call), timed with events in the default bf16 arithmetic and with
+    native MXFP4 activations.  FLOPs = 6 D I rows; utilisation against the dense bf16 and
+    FP4 peaks."""
+    D, I, fmt = cfg["D"], cfg["I"], cfg["fmt"]
+    sel = [i for i in range(w.nb) if int(w.nr[i]) >= min_rows]
+    if not sel:
+        return None
+    nr = np.ascontiguousarray(w.nr[sel], np.int32)
+    xoff = np.ascontiguousarray(w.xoff[sel], np.int32)
+    base = np.concatenate(([0], np.cumsum(w.nr)))
+    pick = np.concatenate([np.arange(base[i], base[i + 1]) for i in sel])
+    rows = np.ascontiguousarray(w.rows[pick], np.int32)
+    rw = np.ascontiguousarray(w.rw[pick], np.float32)
+    lists = []
+    order = (0, 2, 4, 1, 3, 5)
+    b0 = pool.pool.data_ptr()
+    for layer in range(pool.layers):
+        ptrs = [[b0 + (layer * w.nb + i) * pool.stride + int(pool.off[o]) for i in sel]
+                for o in order]
+        lists.append(mvllm_hip.prepare_lists(*ptrs))
+    xg = torch.from_numpy(w.xg).cuda()
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    flops = 6.0 * D * I * float(nr.sum())
+    rec = {"min_rows": min_rows, "experts": len(sel), "rows": int(nr.sum()),
+           "rows_per_expert": [int(n) for n in nr], "flops": flops}
+    for fp4 in (False, True):
+        mvllm_hip.set_option("fp4act", 1 if fp4 else 0)
+
+        def step(s):
+            mvllm_hip.moe_block_dev(len(sel), D, I, fmt, None, None, None, None, None, None, xg,
+                                    xoff, nr, rows, rw, out, T, w.act, w.a, w.b,
+                                    prepared=lists[s % len(lists)])
+        for s in range(warmup):
+            step(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(steps):
+            step(s)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        tf = flops / (ms * 1e-3) / 1e12
+        key = "fp4act" if fp4 else "bf16"
+        rec[key] = {"us_per_call": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                    "mfma_util_bf16": round(tf / BF16_PEAK_TFS, 4),
+                    "mfma_util_fp4": round(tf / FP4_PEAK_TFS, 4)}
+        log(f"hot segments (>= {min_rows} rows: {len(sel)} experts, {int(nr.sum())} rows), "
+            f"{key}: {ms*1e3:.1f} us per call, {tf:.0f} TFLOP/s = "
+            f"{tf / BF16_PEAK_TFS:.3f} of the bf16 peak, {tf / FP4_PEAK_TFS:.3f} of the FP4 peak")
+    mvllm_hip.set_option("fp4act", 0)
+    del xg, out
+    return rec
 
 
 def probe_sizes(np, mvllm_hip, pool, sink, probe_bytes):

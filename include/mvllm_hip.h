@@ -236,7 +236,12 @@ int mvllm_hip_router_dev(const float *x, const float *w, const float *bias, int 
  * 2003-2006, 2074-2090).  fmt 0: f32 W [O][K] on the f32 matrix cores (K % 16, O % 32,
  * 16-byte aligned rows); fmt 4 / 7: W codes [O][K/2] with scales as in moe_block, the
  * input rows as two bf16 terms (2^-17 relative) on the bf16 matrix cores (K % 256,
- * O % 256).  QuantMat's int8 rows (fmt 8) are not taken: 0, use the host. */
+ * O % 256); fmt 8: QuantMat's int8 rows W [O][K] with f32 row scales [O]
+ * (quant::matmul_int8_row, src/quant/quant.cpp:255-268; MVLLM_DENSE_BITS=8), each code
+ * exact in f32 on the f32 matrix cores and the row scale applied once to the finished
+ * sum (K % 16, O % 32, 4-byte aligned codes and scales, 16-byte aligned x).  Calls on
+ * one stream, or ordered by the caller: the int4 / MXFP4 forms share one input buffer
+ * (a call on another stream than the previous one waits for it). */
 int mvllm_hip_linear_dev(int fmt, const void *w, const void *scales, int O, int K,
                          const float *x, int n, float *y, void *stream);
 

@@ -11,6 +11,10 @@
 // of each operand at K offset 4 q, and MFMA step s takes element s of them, so the four
 // steps of a block cover its 16 K indices once.  Waves are independent (no LDS, no
 // barrier); loads of the next block are issued before the current one is multiplied.
+// I8: a linear on QuantMat's int8 rows (fmt 8; quant::matmul_int8_row,
+// src/quant/quant.cpp:255-268): lane (t, q) loads the 4 codes of row t at K offset 4 q,
+// each converts exactly to f32, and the row's f32 scale multiplies the finished sum once,
+// as the reference does.
 #include "mfma_common.h"
 
 #include <algorithm>
@@ -25,6 +29,7 @@ struct F32Item {
 
 struct F32Args {
     const ExpertWork *ew;   // per expert: w[0..2] = gate, up, down f32 [O][K]
+                            // (I8: w[mi] int8 [O][K], s[mi] f32 [O])
     const F32Item *items;   // null: one expert (ew1), items of 16 * MT rows over nrows_all
     ExpertWork ew1;
     int nrows_all;
@@ -37,8 +42,9 @@ struct F32Args {
     float act_a, act_b;
 };
 
-template <bool DUAL, int MT>
+template <bool DUAL, int MT, bool I8 = false>
 __global__ __launch_bounds__(64 * kF32Waves) void k_f32mm(F32Args A) {
+    static_assert(!(I8 && DUAL), "int8 rows: single projections only");
     const int item = blockIdx.x / A.nbn;
     const int nb = blockIdx.x - item * A.nbn;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -66,11 +72,17 @@ __global__ __launch_bounds__(64 * kF32Waves) void k_f32mm(F32Args A) {
         xr[mt] = reinterpret_cast<const float4 *>(A.in + (size_t)src * K) + q;
     }
     const float4 *wr[2];
+    const int *wr8[2];  // I8: 4 codes of row t at K offset 4 q of each 16-wide block
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-        const float *w = static_cast<const float *>(ew.w[DUAL ? m : A.mi]);
         const int row = DUAL ? col0 + t : col0 + 16 * m + t;
-        wr[m] = reinterpret_cast<const float4 *>(w + (size_t)row * K) + q;
+        if constexpr (I8) {
+            const int8_t *w = static_cast<const int8_t *>(ew.w[A.mi]);
+            wr8[m] = reinterpret_cast<const int *>(w + (size_t)row * K) + q;
+        } else {
+            const float *w = static_cast<const float *>(ew.w[DUAL ? m : A.mi]);
+            wr[m] = reinterpret_cast<const float4 *>(w + (size_t)row * K) + q;
+        }
     }
     f4v acc[MT][2];
 #pragma unroll
@@ -78,20 +90,33 @@ __global__ __launch_bounds__(64 * kF32Waves) void k_f32mm(F32Args A) {
         acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
     const int nkb = K >> 4;  // 16-wide K blocks; a block is 4 float4 per row
     float4 xa[2][MT], wb[2][2];
+    int wq[2][2];  // I8: raw codes
     auto load = [&](int kb, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
             xa[buf][mt] = xr[mt][4 * kb];
 #pragma unroll
-        for (int m = 0; m < 2; ++m)
-            wb[buf][m] = wr[m][4 * kb];
+        for (int m = 0; m < 2; ++m) {
+            if constexpr (I8)
+                wq[buf][m] = wr8[m][4 * kb];
+            else
+                wb[buf][m] = wr[m][4 * kb];
+        }
     };
     auto mma = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
-                const float4 a = xa[buf][mt], b = wb[buf][m];
+                float4 b;
+                if constexpr (I8) {
+                    const int v = wq[buf][m];
+                    b = float4{(float)(int8_t)(v & 0xff), (float)(int8_t)((v >> 8) & 0xff),
+                               (float)(int8_t)((v >> 16) & 0xff), (float)(int8_t)(v >> 24)};
+                } else {
+                    b = wb[buf][m];
+                }
+                const float4 a = xa[buf][mt];
                 acc[mt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, acc[mt][m], 0, 0, 0);
                 acc[mt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, acc[mt][m], 0, 0, 0);
                 acc[mt][m] = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, acc[mt][m], 0, 0, 0);
@@ -120,6 +145,10 @@ __global__ __launch_bounds__(64 * kF32Waves) void k_f32mm(F32Args A) {
             float *dst = A.out + (size_t)(jbase + r) * O;
             if constexpr (DUAL) {
                 dst[col0 + t] = mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
+            } else if constexpr (I8) {
+                const float *sc = static_cast<const float *>(ew.s[A.mi]);
+                dst[col0 + t] = acc[mt][0][i] * sc[col0 + t];
+                dst[col0 + 16 + t] = acc[mt][1][i] * sc[col0 + 16 + t];
             } else {
                 dst[col0 + t] = acc[mt][0][i];
                 dst[col0 + 16 + t] = acc[mt][1][i];
@@ -134,8 +163,9 @@ bool f32mm_fits(bool dual, int K, int O) {
 hipError_t launch_f32mm(bool dual, int mt, const ExpertWork *ew, const void *items, int n_items,
                         const ExpertWork *ew1, int nrows_all, const float *in,
                         const int *in_rows, float *out, int mi, int K, int O, int act,
-                        float act_a, float act_b, hipStream_t st) {
-    if (!f32mm_fits(dual, K, O) || (mt != 1 && mt != 2 && mt != 4) || (!items && !ew1))
+                        float act_a, float act_b, hipStream_t st, bool i8) {
+    if (!f32mm_fits(dual, K, O) || (mt != 1 && mt != 2 && mt != 4) || (!items && !ew1) ||
+        (i8 && dual))
         return hipErrorInvalidValue;
     F32Args a{};
     a.ew = ew;
@@ -160,12 +190,16 @@ hipError_t launch_f32mm(bool dual, int mt, const ExpertWork *ew, const void *ite
         return hipSuccess;
     const dim3 grid((unsigned)(n_items * a.nbn)), block(64 * kF32Waves);
 #define MVLLM_F32(D, M) hipLaunchKernelGGL((k_f32mm<D, M>), grid, block, 0, st, a)
-    if (dual) {
+#define MVLLM_I8(M) hipLaunchKernelGGL((k_f32mm<false, M, true>), grid, block, 0, st, a)
+    if (i8) {
+        if (mt == 1) MVLLM_I8(1); else if (mt == 2) MVLLM_I8(2); else MVLLM_I8(4);
+    } else if (dual) {
         if (mt == 1) MVLLM_F32(true, 1); else if (mt == 2) MVLLM_F32(true, 2); else MVLLM_F32(true, 4);
     } else {
         if (mt == 1) MVLLM_F32(false, 1); else if (mt == 2) MVLLM_F32(false, 2); else MVLLM_F32(false, 4);
     }
 #undef MVLLM_F32
+#undef MVLLM_I8
     return hipGetLastError();
 }
 

@@ -190,10 +190,12 @@ hipError_t launch_prep_planes(int fmt, int terms, const float *x, const int *row
 // row j: in_rows[j] (or j).  Requires K % 16 == 0, O % 16 (dual) / % 32 (single) == 0,
 // 16-byte aligned weight and input rows.
 bool f32mm_fits(bool dual, int K, int O);
+// i8 (single only): w[mi] holds int8 rows [O][K] and s[mi] their f32 row scales (QuantMat
+// fmt 8); 4-byte aligned rows.
 hipError_t launch_f32mm(bool dual, int mt, const ExpertWork *ew, const void *items, int n_items,
                         const ExpertWork *ew1, int nrows_all, const float *in,
                         const int *in_rows, float *out, int mi, int K, int O, int act,
-                        float act_a, float act_b, hipStream_t st);
+                        float act_a, float act_b, hipStream_t st, bool i8 = false);
 // Router tail: scores -> sigmoid in place (the mix), choice = mix + bias; then w *= rscale.
 hipError_t launch_route_tail(float *scores, const float *bias, float *choice, int n, int E,
                              hipStream_t st);

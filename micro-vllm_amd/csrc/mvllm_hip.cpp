@@ -2183,20 +2183,27 @@ int mvllm_hip_linear_dev(int fmt, const void *w, const void *scales, int O, int 
     std::lock_guard<std::mutex> lk(C.mu);
     set_err("");
     const bool q = fmt == 4 || fmt == 7;
-    if (!C.ready || !w || !x || !y || n < 1 || (fmt != 0 && !q) || (q && !scales) ||
+    if (!C.ready || !w || !x || !y || n < 1 || (fmt != 0 && fmt != 8 && !q) ||
+        ((q || fmt == 8) && !scales) ||
         (fmt == 0 && (!f32mm_fits(false, K, O) || !aligned(w, 16) || !aligned(x, 16))) ||
+        (fmt == 8 && (!f32mm_fits(false, K, O) || !aligned(w, 4) || !aligned(x, 16) ||
+                      !aligned(scales, 4))) ||
         (q && (K % 256 || O % 256 || !aligned(w, 8) || !aligned(scales, fmt == 4 ? 16 : 8)))) {
         set_err("linear_dev: bad arguments (fmt 0: K % 16, O % 32, 16-byte aligned rows; "
+                "fmt 8: K % 16, O % 32, 4-byte aligned codes and scales, 16-byte aligned x; "
                 "fmt 4/7: K % 256, O % 256, 8-byte aligned codes, aligned scales)");
         return 0;
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     ExpertWork ew{};
-    if (fmt == 0) {
+    if (fmt == 0 || fmt == 8) {
+        // f32 matrix cores on the f32 rows; int8 codes convert exactly and the row scale
+        // applies once per output (quant::matmul_int8_row, src/quant/quant.cpp:255-268)
         ew.w[0] = w;
+        ew.s[0] = scales;
         const int mt = n <= 16 ? 1 : n <= 32 ? 2 : 4;
         HIP_TRY(launch_f32mm(false, mt, nullptr, nullptr, 0, &ew, n, x, nullptr, y, 0, K, O, 0,
-                             0.f, 0.f, st));
+                             0.f, 0.f, st, fmt == 8));
         return 1;
     }
     // quantized: the input rows as two bf16 terms (2^-17 relative), then the grouped GEMM.

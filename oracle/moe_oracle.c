@@ -136,6 +136,20 @@ void orc_matmul_int4_g64(float *y, const float *x, const uint8_t *packed, const 
     }
 }
 
+void orc_matmul_int8_row(float *y, const float *x, const int8_t *q, const float *scales, int S,
+                         int I, int O) {
+    for (int s = 0; s < S; ++s) {
+        const float *xr = x + (size_t)s * (size_t)I;
+        for (int o = 0; o < O; ++o) {
+            const int8_t *qr = q + (size_t)o * (size_t)I;
+            float acc = 0.f;
+            for (int i = 0; i < I; ++i)
+                acc += xr[i] * (float)qr[i];
+            y[(size_t)s * (size_t)O + (size_t)o] = acc * scales[o];
+        }
+    }
+}
+
 void orc_matmul_mxfp4(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
                       int S, int I, int O) {
     const size_t stride = (size_t)((I + 1) / 2);

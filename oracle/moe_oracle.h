@@ -46,6 +46,11 @@ void orc_apply_act(float *g, const float *u, int n, int act, float a, float b);
 void orc_matmul_f32(float *y, const float *x, const float *w, int S, int I, int O);
 void orc_matmul_int4_g64(float *y, const float *x, const uint8_t *packed, const float *scales,
                          int S, int I, int O);
+/* quant::matmul_int8_row (src/quant/quant.cpp:255-268): y[s,o] = (sum_i x[s,i] * q[o,i]) *
+ * scales[o], one sequential f32 sum per output, the row scale applied once after it.  q is
+ * int8 [O][I] (QuantMat fmt 8, src/quant/weight.cpp:38-41,57-61). */
+void orc_matmul_int8_row(float *y, const float *x, const int8_t *q, const float *scales, int S,
+                         int I, int O);
 void orc_matmul_mxfp4(float *y, const float *x, const uint8_t *packed, const uint8_t *scales,
                       int S, int I, int O);
 

@@ -61,6 +61,7 @@ class CpuMoe:
             "matmul_f32": (None, [_p, _p, _p, _i, _i, _i]),
             "matmul_int4_g64": (None, [_p, _p, _p, _p, _i, _i, _i]),
             "matmul_mxfp4": (None, [_p, _p, _p, _p, _i, _i, _i]),
+            "matmul_int8_row": (None, [_p, _p, _p, _p, _i, _i, _i]),
             "sigmoid": (_f, [_f]),
             "clamped_swiglu": (_f, [_f, _f, _f]),
             "situ_glu": (_f, [_f, _f, _f, _f]),
@@ -94,6 +95,7 @@ class CpuMoe:
             L.ref_fp4_activation_qdq.restype = _i
             L.ref_fp4_activation_qdq.argtypes = [_p, _p, _p, _i, _i]
             for name, args in {"quantize_int4_g64": [_p, _i, _i, _p, _p],
+                               "quantize_int8_row": [_p, _i, _i, _p, _p],
                                "pack_mxfp4": [_p, _i, _i, _p, _p],
                                "silu_mul": [_p, _p, _i],
                                "bf16_round_array": [_p, _i],
@@ -170,7 +172,8 @@ class CpuMoe:
 
     # ---- GEMMs ---------------------------------------------------------------
     def matmul(self, fmt, x, w, scales=None):
-        """y[S,O] for fmt 0 (w f32 [O,I]), 4 (w packed u8 [O,(I+1)//2], scales f32) or 7."""
+        """y[S,O] for fmt 0 (w f32 [O,I]), 4 (w packed u8 [O,(I+1)//2], scales f32), 7, or
+        8 (QuantMat's int8 rows: w int8 [O,I], scales f32 [O])."""
         x = np.ascontiguousarray(x, np.float32)
         S, I = x.shape
         O = w.shape[0]
@@ -180,6 +183,9 @@ class CpuMoe:
                                   S, I, O)
         elif fmt == 4:
             self.fn("matmul_int4_g64")(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), S, I, O)
+        elif fmt == 8:
+            self.fn("matmul_int8_row")(_ptr(y), _ptr(x), _ptr(np.ascontiguousarray(w, np.int8)),
+                                       _ptr(np.ascontiguousarray(scales, np.float32)), S, I, O)
         else:
             self.fn("matmul_mxfp4")(_ptr(y), _ptr(x), _ptr(w), _ptr(scales), S, I, O)
         return y

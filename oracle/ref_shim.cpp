@@ -38,6 +38,13 @@ void ref_matmul_mxfp4(float *y, const float *x, const uint8_t *p, const uint8_t 
                       int O) {
     quant::matmul_mxfp4(y, x, p, s, S, I, O);
 }
+void ref_matmul_int8_row(float *y, const float *x, const int8_t *q, const float *s, int S, int I,
+                         int O) {
+    quant::matmul_int8_row(y, x, q, s, S, I, O);
+}
+void ref_quantize_int8_row(const float *w, int O, int I, int8_t *q, float *s) {
+    quant::quantize_int8_row(w, O, I, q, s);
+}
 void ref_quantize_int4_g64(const float *w, int O, int I, uint8_t *p, float *s) {
     quant::quantize_int4_g64(w, O, I, p, s);
 }

@@ -120,14 +120,26 @@ def test_router_matches_host_router(hip, orc, T, D, E, k, rscale, bias):
 
 @pytest.mark.parametrize("fmt,O,K,n", [(0, 2048, 7168, 1), (0, 7168, 2048, 5), (0, 64, 48, 3),
                                        (4, 2048, 6144, 1), (4, 512, 1024, 40),
-                                       (7, 7168, 2048, 3), (7, 256, 512, 70)])
+                                       (7, 7168, 2048, 3), (7, 256, 512, 70),
+                                       (8, 2048, 7168, 1), (8, 7168, 2048, 4),
+                                       (8, 7168, 7168, 1), (8, 96, 48, 37)])
 def test_linear(hip, orc, fmt, O, K, n):
+    """fmt 8 (QuantMat's int8 rows, MVLLM_DENSE_BITS=8) at K3's latent shapes, with codes
+    and scales from the reference's quantizer rule (row amax / 127, clamp +-127) and an
+    all-zero row (scale 0)."""
     say("linear", fmt, O, K, n)
     rng = np.random.default_rng(O + K + n + fmt)
     x = rng.standard_normal((n, K)).astype(np.float32)
     if fmt == 0:
         w = (rng.standard_normal((O, K)) * 0.05).astype(np.float32)
         sc = None
+    elif fmt == 8:
+        wf = (rng.standard_normal((O, K)) * 0.05).astype(np.float32)
+        wf[1] = 0.0
+        amax = np.abs(wf).max(axis=1)
+        sc = (amax / np.float32(127.0)).astype(np.float32)
+        inv = np.where(sc > 0, np.float32(1.0) / np.where(sc > 0, sc, 1), 0).astype(np.float32)
+        w = np.clip(np.round(wf * inv[:, None]), -127, 127).astype(np.int8)
     else:
         e = expert_arrays(rng, fmt, K, O)   # gate: [O, K] codes and scales
         w, sc = e["gp"], e["gs"]
@@ -138,14 +150,18 @@ def test_linear(hip, orc, fmt, O, K, n):
     exp = orc.matmul(fmt, x, w, sc)
     err = npref.rel_err(got, exp)
     say("  rel_err", err)
-    assert err < (TOL_F32 if fmt == 0 else 1e-4)
+    assert err < (TOL_F32 if fmt in (0, 8) else 1e-4)
 
 
-def test_linear_refuses_int8_and_odd_shapes(hip):
-    """QuantMat's int8 rows (fmt 8) and shapes the kernels do not take return 0 (the host
-    runs them), with a message."""
+def test_linear_refuses_odd_shapes(hip):
+    """Shapes and formats the kernels do not take return 0 (the host runs them), with a
+    message."""
     buf = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
-    assert hip.lib().mvllm_hip_linear_dev(8, buf.data_ptr(), buf.data_ptr(), 256, 256,
+    assert hip.lib().mvllm_hip_linear_dev(8, buf.data_ptr(), buf.data_ptr(), 100, 256,
+                                          buf.data_ptr(), 1, buf.data_ptr(), None) == 0
+    assert hip.lib().mvllm_hip_linear_dev(8, buf.data_ptr(), None, 256, 256,
+                                          buf.data_ptr(), 1, buf.data_ptr(), None) == 0
+    assert hip.lib().mvllm_hip_linear_dev(5, buf.data_ptr(), buf.data_ptr(), 256, 256,
                                           buf.data_ptr(), 1, buf.data_ptr(), None) == 0
     assert hip.lib().mvllm_hip_linear_dev(4, buf.data_ptr(), buf.data_ptr(), 100, 256,
                                           buf.data_ptr(), 1, buf.data_ptr(), None) == 0

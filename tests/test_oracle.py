@@ -140,7 +140,15 @@ def test_dequant_bit_exact_closed_form(orc, fmt, K):
     assert np.array_equal(w.view(np.uint32), exp.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", [0, 4, 7])
+def test_kat_matmul_int8_row(orc):
+    """quant::matmul_int8_row: the row scale multiplies the whole sum, once."""
+    x = np.array([[1, 2, -1]], np.float32)
+    q = np.array([[1, 0, 3], [0, -3, 127], [-127, 1, 0]], np.int8)
+    s = np.array([0.5, 2.0, 0.25], np.float32)
+    assert orc.matmul(8, x, q, s).tolist() == [[-1.0, -266.0, -31.25]]
+
+
+@pytest.mark.parametrize("fmt", [0, 4, 7, 8])
 def test_matmul_vs_f64(orc, fmt):
     rng = np.random.default_rng(11 + fmt)
     S, K, O = 3, 160, 24  # non-square: a transposed operand cannot pass
@@ -150,11 +158,18 @@ def test_matmul_vs_f64(orc, fmt):
     elif fmt == 4:
         w = rng.integers(0, 256, size=(O, K // 2), dtype=np.uint8)
         s = rng.uniform(0.005, 0.02, size=(O, (K + 63) // 64)).astype(np.float32)
-    else:
+    elif fmt == 7:
         w = rng.integers(0, 256, size=(O, K // 2), dtype=np.uint8)
         s = rng.integers(118, 125, size=(O, K // 32), dtype=np.uint8)
+    else:
+        w = rng.integers(-127, 128, size=(O, K), dtype=np.int8)
+        s = rng.uniform(0.001, 0.01, size=O).astype(np.float32)
     y = orc.matmul(fmt, x, w, s)
-    ref = x.astype(np.float64) @ npref.dequant(fmt, w, s, K).astype(np.float64).T
+    if fmt == 8:
+        wd = w.astype(np.float64) * s.astype(np.float64)[:, None]
+    else:
+        wd = npref.dequant(fmt, w, s, K).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T
     assert npref.rel_err(y, ref) < 20 * K * F32_EPS / np.sqrt(K)
 
 
@@ -337,12 +352,19 @@ def test_ref_scalars_bit_exact(orc, ref):
 
 
 @pytest.mark.parametrize("fmt,S,K,O", [(0, 3, 64, 17), (4, 2, 256, 9), (4, 3, 100, 5),
-                                       (7, 2, 224, 11), (7, 1, 45, 6)])
+                                       (7, 2, 224, 11), (7, 1, 45, 6), (8, 3, 200, 13),
+                                       (8, 1, 7, 5)])
 def test_ref_matmul_bit_exact(orc, ref, fmt, S, K, O):
     rng = np.random.default_rng(S * K + O)
     x = rng.standard_normal((S, K)).astype(np.float32)
     if fmt == 0:
         w, s = rng.standard_normal((O, K)).astype(np.float32), None
+    elif fmt == 8:  # codes and scales from the reference's own quantize_int8_row
+        wf = rng.standard_normal((O, K)).astype(np.float32)
+        wf[0] = 0.0  # an all-zero row: scale 0, codes 0
+        w, s = np.zeros((O, K), np.int8), np.zeros(O, np.float32)
+        ref.lib.ref_quantize_int8_row(wf.ctypes.data, O, K, w.ctypes.data, s.ctypes.data)
+        assert s[0] == 0 and not w[0].any() and np.abs(w).max() == 127
     elif fmt == 4:
         w = rng.integers(0, 256, size=(O, (K + 1) // 2), dtype=np.uint8)
         s = rng.uniform(0.005, 0.02, size=(O, (K + 63) // 64)).astype(np.float32)
