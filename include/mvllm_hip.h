@@ -300,9 +300,13 @@ int mvllm_hip_slab_free(long long slab);
  *      src/store/expert_store.hpp:71-175).  Blobs are keyed by (layer, eid). -- */
 
 /* Page-locked host memory for ExpertStore slots (replaces aligned_alloc_pages,
- * src/io/file_io.cpp:95, so promotion copies are truly asynchronous). */
+ * src/io/file_io.cpp:95, so promotion copies are truly asynchronous).  NULL (with the
+ * error text set) when the runtime refuses, e.g. without a device: the caller keeps its
+ * own allocator then. */
 void *mvllm_hip_host_alloc(size_t bytes);
-void mvllm_hip_host_free(void *p);
+/* Frees a block from mvllm_hip_host_alloc: 1.  Any other pointer (NULL included) is left
+ * alone: 0, so a caller with a fallback allocator frees it with that one. */
+int mvllm_hip_host_free(void *p);
 
 /* Sets the HBM budget of the expert tier (bytes; default 64 GiB). */
 int mvllm_hip_set_expert_budget(size_t bytes);

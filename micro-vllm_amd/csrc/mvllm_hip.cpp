@@ -1678,14 +1678,16 @@ void *mvllm_hip_host_alloc(size_t bytes) {
     return p;
 }
 
-void mvllm_hip_host_free(void *p) {
+int mvllm_hip_host_free(void *p) {
     if (!p)
-        return;
+        return 0;
     {
         std::lock_guard<std::mutex> lk(g_host_mu);
-        g_host_blocks.erase(reinterpret_cast<uintptr_t>(p));
+        if (g_host_blocks.erase(reinterpret_cast<uintptr_t>(p)) == 0)
+            return 0;  // not ours: the caller's own allocator frees it
     }
     (void)hipHostFree(p);
+    return 1;
 }
 
 int mvllm_hip_set_expert_budget(size_t bytes) {

@@ -50,7 +50,7 @@ _SIGS = {
     "mvllm_moe_segments": (_i, [_p, _p, _i, _i, _p, _p, _p, _p, _p, _i, _i, _p]),
     "mvllm_expert_geom": (_ll, [_i, _i, _i, _p]),
     "mvllm_hip_host_alloc": (_p, [_sz]),
-    "mvllm_hip_host_free": (None, [_p]),
+    "mvllm_hip_host_free": (_i, [_p]),
     "mvllm_hip_set_expert_budget": (_i, [_sz]),
     "mvllm_hip_promote": (_i, [_p, _sz, _i, _i]),
     "mvllm_hip_evict": (_i, [_i, _i]),
