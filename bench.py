@@ -137,16 +137,21 @@ def measure(np, torch, mvllm_hip, synth, name, T, steps, warmup, pool_gb, fp4act
     host_us = (st1["host_ms"] - st0["host_ms"]) / steps * 1e3
     wait_us = (st1["host_wait_ms"] - st0["host_wait_ms"]) / steps * 1e3
     # the host's own work per call (plan + launches) with the device idle: in the loop
-    # above the host runs ahead and also waits on a full launch queue
-    n_iso = min(steps, 10)
-    iso_ms = 0.0
+    # above the host runs ahead and also waits on a full launch queue.  The median of 20
+    # calls, each after a synchronize: the first calls after the timed loop pay a thread
+    # wake-up several times the steady cost
+    n_iso = min(steps, 20)
+    iso, plan = [], []
     for s in range(n_iso):
         torch.cuda.synchronize()
-        h0 = mvllm_hip.stats()["host_ms"]
+        h0 = mvllm_hip.stats()
         step(s)
-        iso_ms += mvllm_hip.stats()["host_ms"] - h0
+        h1 = mvllm_hip.stats()
+        iso.append(h1["host_ms"] - h0["host_ms"])
+        plan.append(h1["host_plan_ms"] - h0["host_plan_ms"])
     torch.cuda.synchronize()
-    iso_us = iso_ms / n_iso * 1e3
+    iso_us = float(np.median(iso)) * 1e3
+    plan_us = float(np.median(plan)) * 1e3
     # per-phase kernel durations: a second pass with HIP events around each phase
     mvllm_hip.set_option("timing", 1)
     mvllm_hip.stats_reset()
@@ -179,7 +184,7 @@ def measure(np, torch, mvllm_hip, synth, name, T, steps, warmup, pool_gb, fp4act
         "workload": f"{name} {cfg['desc']}, T={T}" + (", native MXFP4 activations" if fp4act else ""),
         "value": round(T / (ms_step * 1e-3), 2), "unit": "tokens/s",
         "ms_per_step": round(ms_step, 6), "wall_ms_per_step": round(wall / steps * 1e3, 6),
-        "host_us_per_call": round(iso_us, 1),
+        "host_us_per_call": round(iso_us, 1), "host_plan_us_per_call": round(plan_us, 1),
         "host_loop_us_per_call": round(host_us - wait_us, 1),
         "host_wait_us_per_call": round(wait_us, 1), "dtype": dtype,
         "experts": int(w.nb), "rows": rows, "max_rows_per_expert": int(max(nr)),
@@ -205,7 +210,7 @@ def measure(np, torch, mvllm_hip, synth, name, T, steps, warmup, pool_gb, fp4act
         "pool_gib": round(pool.gib, 2),
     }
     log(f"[{wl}] step {ms_step*1e3:.1f} us (wall {wall/steps*1e6:.1f} us, host {iso_us:.1f} "
-        f"us/call with the device idle; in the loop {host_us - wait_us:.1f} us/call + "
+        f"us/call with the device idle (median), {plan_us:.1f} of it before the launches; in the loop {host_us - wait_us:.1f} us/call + "
         f"{wait_us:.1f} us blocked on plan slots): prep {ph['prep']:.1f}, gate/up {t_gu:.1f}, down "
         f"{ph['down']:.1f}, combine {ph['combine']:.1f} us; gate/up {gu_gbs:.0f} GB/s "
         f"(binding roof {lb_gu:.1f} us, {lb_gu/t_gu:.3f}); call {lb_call/(ms_step*1e3):.3f} "

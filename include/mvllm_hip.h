@@ -381,6 +381,9 @@ int mvllm_hip_tier_table_done(int layer, void *stream);
  *     within mvllm_hip_set_expert_budget
  *  18 (gauge) of 17, the blocks of blobs dropped while their layer's tier tables are
  *     open, held until mvllm_hip_tier_table_done recycles them
+ *  19 host ms of 15 spent in mvllm_hip_moe_block_dev(_noalloc) before its first kernel
+ *     launch: the plan, the call's configuration, buffers and the plan's upload (the
+ *     rest of 15 is the launches)
  * Kernel times are filled only with option "timing"=1.  Returns the count written
  * (<= n). */
 int mvllm_hip_stats(double *vals, int n);

@@ -6,6 +6,8 @@
 #include <algorithm>
 #include <cmath>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 namespace mvllm_hip {
 
@@ -34,6 +36,29 @@ size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks,
     return dec_lds_plan(fmt, K, rmax, terms, ks, nt, nullptr);
 }
 
+// Raises kernel f's dynamic LDS limit to `lds` bytes once per process: up to 64 KiB needs
+// no attribute, and a limit already raised that far is not set again (the attribute call
+// costs host time on every decode launch otherwise).  The library's entry points hold its
+// lock around every launch, which guards this table.
+static hipError_t lds_limit(const void *f, size_t lds) {
+    static std::vector<std::pair<const void *, size_t>> set;
+    if (lds <= 65536)
+        return hipSuccess;
+    for (auto &p : set)
+        if (p.first == f && p.second >= lds)
+            return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess)
+        return e;
+    for (auto &p : set)
+        if (p.first == f) {
+            p.second = lds;
+            return e;
+        }
+    set.emplace_back(f, lds);
+    return e;
+}
+
 template <int FMT, bool DUAL, int TERMS, int KS, int NT>
 static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const DecDescK *inl) {
     const size_t lds = mfma_dec_lds_bytes(FMT, a.K, a.rmax, TERMS, DUAL, KS, NT);
@@ -59,8 +84,7 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const Dec
         constexpr bool HI = decltype(has_inl)::value;
         const void *f = HI && inl ? reinterpret_cast<const void *>(kern_inl)
                                   : reinterpret_cast<const void *>(kern);
-        hipError_t e =
-            hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        hipError_t e = lds_limit(f, lds);
         if (e != hipSuccess)
             return e;
         if constexpr (HI) {

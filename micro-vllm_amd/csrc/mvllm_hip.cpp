@@ -155,6 +155,67 @@ struct TimedCall {
     hipEvent_t ev[6];
 };
 
+// ---- plan -------------------------------------------------------------------------
+
+struct Plan {
+    std::vector<ExpertWork> ew;     // active experts
+    std::vector<int> src_expert;    // ew index -> caller's expert index e
+    std::vector<int> xrow;          // compact row -> row of xg
+    std::vector<int> dest;          // compact row -> destination row of out
+    std::vector<float> w;           // compact row -> combine weight
+    std::vector<int> tok_ptr, ent_row, out_row;
+    std::vector<float> ent_w;
+    int nr_max = 0;
+    int D = 0, I = 0;
+    std::vector<int> pos, order;  // build_plan's sort scratch
+    // empties the plan, keeping every vector's storage (no heap traffic per call)
+    void reset() {
+        for (auto *v : {&src_expert, &xrow, &dest, &tok_ptr, &ent_row, &out_row})
+            v->clear();
+        ew.clear();
+        w.clear();
+        ent_w.clear();
+        nr_max = D = I = 0;
+    }
+};
+
+// How one call runs: the matrix-core path for both projections (activation planes,
+// items of up to rmax rows), or the exact element-wise kernels.
+struct PhaseCfg {
+    int rmax = 0, ks = 1, nt = 1;  // rows per item, K split, tiles per wave
+    size_t it0 = 0, it_split = 0, it1 = 0;  // item range; [it0, it_split) = experts < split
+};
+
+// Row-block class of the grouped GEMM: items of 16 * mt rows at most, in
+// [it0, it1) of CallCfg::items; items of experts < split come first, up to it_split.
+struct GemmCls {
+    int mt = 0;
+    size_t it0 = 0, it_split = 0, it1 = 0;
+};
+
+struct CallCfg {
+    bool mfma = false;        // decode-shaped matrix-core kernels
+    bool gemm = false;        // grouped GEMM (prefill-shaped)
+    bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
+    bool f32 = false;         // fmt 0: the f32 matrix-core GEMM (kern_f32.hip)
+    bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
+    bool w16 = false;         // every weight pointer 16-byte aligned (the wide-tile GEMM)
+    int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
+    PhaseCfg gu, dn;
+    std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
+    GemmCls gcls[kGemmClasses];
+    int n_gcls = 0;
+    std::vector<int> per[kGemmClasses];  // plan_gemm's per-class scratch
+    // the default configuration, keeping the vectors' storage
+    void reset() {
+        mfma = gemm = fp4 = f32 = atomic_combine = w16 = false;
+        terms = 2;
+        gu = dn = PhaseCfg();
+        items.clear();
+        n_gcls = 0;
+    }
+};
+
 struct Ctx {
     std::mutex mu;
     bool ready = false;
@@ -173,6 +234,9 @@ struct Ctx {
     DevBuf Lp;  // planes of mvllm_hip_linear_dev's input rows
     DevBuf Rp;  // device plan of mvllm_hip_moe_block_routed_dev
     HostBuf hx, ho;
+    // the plan and configuration of the current call (every entry holds mu), reused
+    Plan plan;
+    CallCfg cfg;
     // Plan slots, reused in groups of kGroup: one event after a group's last call guards
     // the reuse of all its slots.  A group whose last call did not reach finish_call is
     // drained before its slots are reused (open_last).
@@ -215,7 +279,7 @@ struct Ctx {
     hipEvent_t tier_ready = nullptr;  // copy stream: every promotion enqueued so far
     std::vector<std::pair<size_t, void *>> pending_free;
     // stats
-    double stats[19] = {0};
+    double stats[20] = {0};
     std::vector<TimedCall> timed;
 };
 
@@ -248,20 +312,6 @@ long long res_key(int layer, int eid) {
     return (static_cast<long long>(layer) << 32) | static_cast<unsigned>(eid);
 }
 
-// ---- plan -------------------------------------------------------------------------
-
-struct Plan {
-    std::vector<ExpertWork> ew;     // active experts
-    std::vector<int> src_expert;    // ew index -> caller's expert index e
-    std::vector<int> xrow;          // compact row -> row of xg
-    std::vector<int> dest;          // compact row -> destination row of out
-    std::vector<float> w;           // compact row -> combine weight
-    std::vector<int> tok_ptr, ent_row, out_row;
-    std::vector<float> ent_w;
-    int nr_max = 0;
-    int D = 0, I = 0;
-};
-
 size_t piece_bytes(int fmt, int piece, int D, int I) {
     // piece: 0 gate/up packed, 1 gate/up scales, 2 down packed, 3 down scales
     const size_t O = piece < 2 ? (size_t)I : (size_t)D;
@@ -278,7 +328,7 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
                 const void *const *u, const void *const *d, const float *const *gs,
                 const float *const *us, const float *const *ds, const int *xoff, const int *nr,
                 const int *rows, const float *rw, int S) {
-    P = Plan();
+    P.reset();
     P.D = D;
     P.I = Iinter;
     size_t total = 0;
@@ -334,7 +384,8 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
     P.ent_row.resize(R);
     P.ent_w.resize(R);
     if ((size_t)max_dest + 1 <= 4 * (size_t)R + 4096) {
-        std::vector<int> pos((size_t)max_dest + 2, 0);
+        std::vector<int> &pos = P.pos;
+        pos.assign((size_t)max_dest + 2, 0);
         for (int j = 0; j < R; ++j)
             ++pos[(size_t)P.dest[j] + 1];
         for (int t = 0; t <= max_dest; ++t) {
@@ -350,7 +401,8 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
             P.ent_w[at] = P.w[j];
         }
     } else {
-        std::vector<int> order(R);
+        std::vector<int> &order = P.order;
+        order.resize(R);
         for (int j = 0; j < R; ++j)
             order[j] = j;
         std::stable_sort(order.begin(), order.end(),
@@ -369,34 +421,6 @@ void build_plan(Plan &P, int nb, int D, int Iinter, int fmt, const void *const *
 }
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
-
-// How one call runs: the matrix-core path for both projections (activation planes,
-// items of up to rmax rows), or the exact element-wise kernels.
-struct PhaseCfg {
-    int rmax = 0, ks = 1, nt = 1;  // rows per item, K split, tiles per wave
-    size_t it0 = 0, it_split = 0, it1 = 0;  // item range; [it0, it_split) = experts < split
-};
-
-// Row-block class of the grouped GEMM: items of 16 * mt rows at most, in
-// [it0, it1) of CallCfg::items; items of experts < split come first, up to it_split.
-struct GemmCls {
-    int mt = 0;
-    size_t it0 = 0, it_split = 0, it1 = 0;
-};
-
-struct CallCfg {
-    bool mfma = false;        // decode-shaped matrix-core kernels
-    bool gemm = false;        // grouped GEMM (prefill-shaped)
-    bool fp4 = false;         // grouped GEMM on native MXFP4 activations (option fp4act)
-    bool f32 = false;         // fmt 0: the f32 matrix-core GEMM (kern_f32.hip)
-    bool atomic_combine = false;  // decode kernels: combine folded into down (float atomics)
-    bool w16 = false;         // every weight pointer 16-byte aligned (the wide-tile GEMM)
-    int terms = 2;            // bf16 terms per activation (3: exact, 2: 2^-17, 1: bf16)
-    PhaseCfg gu, dn;
-    std::vector<int> items;   // {expert, r0, nrow, 0} records of both phases
-    GemmCls gcls[kGemmClasses];
-    int n_gcls = 0;
-};
 
 // Does the decode kernel take this phase shape (K split ks, nt tiles per wave)?
 bool dec_fits(int fmt, int K, int O, int rmax, int terms, bool dual, int ks, int nt) {
@@ -487,7 +511,9 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
     // bf16 one-term GEMM: an expert of 33-64 rows (a last block of that size) runs as two
     // 32-row items of the two-workgroups-per-CU class, which read its weights together
     const bool split64 = !cc.f32 && !cc.fp4 && cc.terms == 1 && max_mt >= 4;
-    std::vector<int> per[kGemmClasses];  // class index = log2(mt)
+    std::vector<int> *per = cc.per;  // class index = log2(mt)
+    for (int c = 0; c < kGemmClasses; ++c)
+        per[c].clear();
     size_t split_at[kGemmClasses] = {};
     for (size_t i = 0; i < P.ew.size(); ++i) {
         if (i == split)
@@ -545,7 +571,7 @@ void plan_gemm(CallCfg &cc, const Plan &P, size_t split, int fmt) {
 // (no float-atomic fold into the down kernel).
 void plan_call(const Ctx &C, CallCfg &cc, const Plan &P, int fmt, int D, int I, size_t split,
                const void *in, bool ordered) {
-    cc = CallCfg();
+    cc.reset();
     // bf16 terms per activation: 2 (default) represents each f32 activation to 2^-17
     // relative, 3 exactly (mode 1), 1 is plain bf16 (mode 2).  The grouped GEMM takes
     // 1 term by default (bf16 activations, the prefill arithmetic) and 2 in mode 1.
@@ -1165,13 +1191,13 @@ int dev_call(Ctx &C, int nb, int D, int Iinter, int fmt, const void *const *g,
              const int *nr, const int *rows, const float *rw, float *out, int S, int act,
              float act_a, float act_b, hipStream_t st, bool noalloc) {
     HostClock hc(&C.stats[15]);
-    Plan P;
+    Plan &P = C.plan;
     build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
     C.stats[0] += 1;
     if (P.ew.empty())
         return 1;
     const size_t R = P.xrow.size();
-    CallCfg cc;
+    CallCfg &cc = C.cfg;
     plan_call(C, cc, P, fmt, D, Iinter, P.ew.size(), xg, C.combine_ordered != 0);
     Bufs B;
     if (noalloc) {  // carve the buffers out of the scratch array, after the plan region
@@ -1199,6 +1225,8 @@ int dev_call(Ctx &C, int nb, int D, int Iinter, int fmt, const void *const *g,
     if (!upload_plan(C, P, cc, st, dp, false, noalloc ? C.scratch_ptr : nullptr,
                      noalloc ? kScratchPlan : 0))
         return 0;
+    C.stats[19] += std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() -
+                                                             hc.t0).count();
     if (!run_phases(C, P, cc, dp, B, fmt, D, Iinter, act, act_a, act_b, xg, dp.xrow, out, st,
                     P.ew.size(), nullptr, !noalloc))
         return 0;
@@ -1500,7 +1528,7 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     if (!args_ok(nb, D, fmt, xg, xoff, nr, out))
         return 0;
     HostClock hc(&C.stats[15]);
-    Plan P;
+    Plan &P = C.plan;
     build_plan(P, nb, D, Iinter, fmt, g, u, d, gs, us, ds, xoff, nr, rows, rw, S);
     C.stats[0] += 1;
     if (P.ew.empty())
@@ -1640,7 +1668,7 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
     std::vector<int> dest_rows = P.out_row;
     for (size_t t = 0; t < T; ++t)
         P.out_row[t] = static_cast<int>(t);
-    CallCfg cc;
+    CallCfg &cc = C.cfg;
     plan_call(C, cc, P, fmt, D, Iinter, hit.size(), C.Xc.p, true);
     Bufs B;
     HIP_TRY(get_bufs(C, cc, R, D, Iinter, B));
@@ -1952,7 +1980,7 @@ int mvllm_hip_stats(double *vals, int n) {
     C.timed.clear();
     C.stats[17] = static_cast<double>(C.used_bytes + C.parked_bytes);
     C.stats[18] = static_cast<double>(C.parked_bytes);
-    const int m = std::min(n, 19);
+    const int m = std::min(n, 20);
     for (int i = 0; i < m; ++i)
         vals[i] = C.stats[i];
     return m;

@@ -28,7 +28,7 @@ ACT_SILU, ACT_CLAMP_SWIGLU, ACT_SITU = 0, 1, 2
 STAT_NAMES = ["calls", "rows", "h2d_weight_bytes", "h2d_act_bytes", "d2h_bytes", "promotions",
               "resident_hits", "misses", "evictions", "ms_gate_up", "ms_down", "ms_combine",
               "ms_prep", "launches_gate_up", "launches_down", "host_ms", "host_wait_ms",
-              "tier_bytes", "tier_parked_bytes"]
+              "tier_bytes", "tier_parked_bytes", "host_plan_ms"]
 
 _i, _f, _p, _sz, _ll = C.c_int, C.c_float, C.c_void_p, C.c_size_t, C.c_longlong
 _pp = C.POINTER(C.c_void_p)
