@@ -200,12 +200,18 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
  * HBM tier's blobs); an id outside [0, n_table), a null entry or a misaligned one
  * consumes its rows without writing (the reference's null-expert rule,
  * src/gpu/metal_ops.cpp:291-296).  x [S][D] token rows, out [S][D] accumulated with
- * += in expert order (src/gpu/metal_ops.cpp:328-339).  The plan (expert work, grouped-
- * GEMM items, the combine lists) is built by kernels; launches are sized for the caps
- * (cap_experts segments, cap_rows compact rows) and their surplus workgroups exit.
- * Arithmetic: the grouped GEMM with two bf16 terms per activation (2^-17) when cap_rows
- * <= 256, one above (mode option 1: always two, 2: always one).  fmt 4 / 7, D and Iinter
- * multiples of 256, 1 <= S <= 65535.  status (device int, may be NULL) receives 0, or 2
+ * += in expert order (src/gpu/metal_ops.cpp:328-339).  The plan is built by kernels;
+ * launches are sized for the caps (cap_experts segments, cap_rows compact rows) and their
+ * surplus workgroups exit.  Two paths:
+ *   S <= 16 (decode): the decode kernels of mvllm_hip_moe_block_dev's decode-shaped calls
+ *     (two bf16 terms per activation; mode 1 three, mode 2 one) on items of up to S rows
+ *     of one expert, and, as there, the combine folded into the down kernel as float
+ *     atomics (out row sums in any expert order) unless option combine_ordered is 1;
+ *     three launches.  Option gemm=1 takes the grouped path instead.
+ *   otherwise: the grouped GEMM with two bf16 terms per activation (2^-17) when cap_rows
+ *     <= 256, one above (mode option 1: always two, 2: always one), and the ordered
+ *     combine on lists built by kernels.
+ * fmt 4 / 7, D and Iinter multiples of 256, 1 <= S <= 65535.  status (device int, may be NULL) receives 0, or 2
  * when a blob address was not 256-byte aligned.  Enqueued on `stream`; 1 enqueued. */
 int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const *table,
                                    int n_table, const int *counts, const int *eids,

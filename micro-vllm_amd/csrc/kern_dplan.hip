@@ -10,6 +10,8 @@
 //             liveness, and its grouped-GEMM items (full blocks of BM rows in the top
 //             class, the remainder in the smallest class that holds it), written per
 //             class in expert order by a workgroup scan, with the class item counts;
+//   k_dplan_dec  the same for decode-shaped calls: the decode kernels' descriptors (items
+//             of up to rmax rows, a gate/up and a down descriptor each) and their count;
 //   k_csr_*   the combine lists: per out row t, the compact rows j with rows[j] == t of
 //             experts that are present, in ascending j (= the reference's expert order,
 //             src/gpu/metal_ops.cpp:328-339): count, scan, place, then a per-row sort.
@@ -25,6 +27,33 @@ constexpr int kPlanThreads = 1024;
 
 __device__ __forceinline__ int dplan_class(int n) {
     return n <= 16 ? 0 : n <= 32 ? 1 : n <= 64 ? 2 : 3;
+}
+
+// The blob of expert e (null when e is outside the table, its entry is null or not
+// 256-byte aligned: err = 2 for the last) and the live row count of a segment at compact
+// row x0 with nr rows (out of nrows).
+template <class Args>
+__device__ __forceinline__ const char *dplan_blob(const Args &A, int e, int nrows, int x0,
+                                                  int nr, int &n) {
+    n = (x0 < 0 || x0 > nrows) ? 0 : max(0, min(nr, nrows - max(x0, 0)));
+    const char *blob = (e >= 0 && e < A.n_table) ? static_cast<const char *>(A.table[e])
+                                                 : nullptr;
+    if (reinterpret_cast<uintptr_t>(blob) & 255) {  // not a slab / tier blob address
+        *A.err = 2;
+        blob = nullptr;
+    }
+    return blob;
+}
+
+// Segment i's blob, first compact row x0 and live row count n (dplan_blob).
+template <class Args>
+__device__ __forceinline__ const char *dplan_segment(const Args &A, int i, int nrows, int &x0,
+                                                     int &n) {
+    // the three independent loads first, then the table read that depends on one
+    const int e = A.eids[i];
+    x0 = A.xoff[i];
+    const int nr = A.nr[i];
+    return dplan_blob(A, e, nrows, x0, nr, n);
 }
 
 __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
@@ -43,18 +72,8 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
     const int s0 = min(nb, tid * per), s1 = min(nb, s0 + per);
     int cnt[4] = {0, 0, 0, 0};
     for (int i = s0; i < s1; ++i) {
-        const int e = A.eids[i];
-        const char *blob = (e >= 0 && e < A.n_table) ? static_cast<const char *>(A.table[e])
-                                                     : nullptr;
-        if (reinterpret_cast<uintptr_t>(blob) & 255) {  // not a slab / tier blob address
-            *A.err = 2;
-            blob = nullptr;
-        }
-        const int x0 = A.xoff[i];
-        int n = A.nr[i];
-        if (x0 < 0 || x0 > nrows)
-            n = 0;
-        n = max(0, min(n, nrows - max(x0, 0)));
+        int x0, n;
+        const char *blob = dplan_segment(A, i, nrows, x0, n);
         ExpertWork w{};
         if (blob) {
             w.w[0] = blob + A.off[0];
@@ -122,6 +141,104 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
     }
     if (tid < 4)
         A.n_items[tid] = min(tot[tid], A.item_cap[tid]);
+}
+
+// Decode-shaped calls: items of up to rmax rows of each live segment, in segment order,
+// each with the gate/up descriptor (the input row of each item row: its out row, x being
+// [S][D]; 0 for a row whose out row is out of range, whose H is then never used) and the
+// down descriptor (out row and combine weight of each item row, -1 for such a row: the
+// folded combine skips it).  One workgroup: the item counts of each thread's segments,
+// a workgroup scan, then the descriptors.
+__global__ __launch_bounds__(kPlanThreads) void k_dplan_dec(DPlanDecArgs A) {
+    __shared__ int wsum[kPlanThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // segment tid's fields, loaded with the counts before they are known (calls of at most
+    // kPlanThreads segments have one a thread: the plan's dependent reads are then the
+    // counts and these, the blob table, the rows, nothing more)
+    int e_t = -1, x_t = 0, nr_t = 0;
+    if (tid < A.cap_e) {
+        e_t = A.eids[tid];
+        x_t = A.xoff[tid];
+        nr_t = A.nr[tid];
+    }
+    const int nb = min(max(A.counts[0], 0), A.cap_e);
+    const int nrows = min(max(A.counts[1], 0), A.cap_rows);
+    for (int j = tid; j < nrows; j += kPlanThreads)
+        A.row_ok[j] = 0;
+    if (tid == 0)
+        *A.err = 0;
+    __syncthreads();
+    const int per = (nb + kPlanThreads - 1) / kPlanThreads;
+    const int s0 = min(nb, tid * per), s1 = min(nb, s0 + per);
+    // segment tid's blob, read once (the second pass reuses it)
+    const char *b_t = nullptr;
+    int n_t = 0;
+    if (s0 <= tid && tid < s1)
+        b_t = dplan_blob(A, e_t, nrows, x_t, nr_t, n_t);
+    auto segment = [&](int i, int &x0, int &n) -> const char * {
+        if (i == tid) {
+            x0 = x_t;
+            n = n_t;
+            return b_t;
+        }
+        return dplan_segment(A, i, nrows, x0, n);
+    };
+    int cnt = 0;
+    for (int i = s0; i < s1; ++i) {
+        int x0, n;
+        if (!segment(i, x0, n) || n == 0)
+            continue;
+        for (int j = x0; j < x0 + n; ++j)
+            A.row_ok[j] = 1;
+        cnt += (n + A.rmax - 1) / A.rmax;
+    }
+    int incl = cnt;  // inclusive scan within the wave, then over the waves' sums
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o)
+            incl += v;
+    }
+    if (lane == 63)
+        wsum[wave] = incl;
+    __syncthreads();
+    int pos = incl - cnt, tot = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) {
+        pos += w < wave ? wsum[w] : 0;
+        tot += wsum[w];
+    }
+    for (int i = s0; i < s1; ++i) {
+        int x0, n;
+        const char *blob = segment(i, x0, n);
+        if (!blob || n == 0)
+            continue;
+        for (int r0 = 0; r0 < n; r0 += A.rmax, ++pos) {
+            if (pos >= A.cap_items) {
+                *A.err = 1;
+                continue;
+            }
+            const int nrow = min(A.rmax, n - r0), jb = x0 + r0;
+            DecDesc g{}, d{};
+            g.w[0] = blob + A.off[0];
+            g.s[0] = blob + A.off[1];
+            g.w[1] = blob + A.off[2];
+            g.s[1] = blob + A.off[3];
+            d.w[0] = d.w[1] = blob + A.off[4];
+            d.s[0] = d.s[1] = blob + A.off[5];
+            g.jbase = d.jbase = jb;
+            g.nrow = d.nrow = nrow;
+            for (int r = 0; r < nrow; ++r) {
+                const int t = A.rows[jb + r];
+                const bool ok = t >= 0 && t < A.S;
+                g.rows[r] = ok ? t : 0;
+                d.rows[r] = ok ? t : -1;
+                d.wts[r] = A.rw[jb + r];
+            }
+            A.gu[pos] = g;
+            A.dn[pos] = d;
+        }
+    }
+    if (tid == 0)
+        *A.n_items = min(tot, A.cap_items);
 }
 
 // ---- the combine lists -----------------------------------------------------------
@@ -216,6 +333,13 @@ __global__ void k_csr_sort(CsrArgs A) {
 
 hipError_t launch_dplan(const DPlanArgs &a, hipStream_t st) {
     hipLaunchKernelGGL(k_dplan, dim3(1), dim3(kPlanThreads), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_dplan_dec(const DPlanDecArgs &a, hipStream_t st) {
+    if (a.rmax < 1 || a.rmax > 16 || a.cap_items < 1)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_dplan_dec, dim3(1), dim3(kPlanThreads), 0, st, a);
     return hipGetLastError();
 }
 

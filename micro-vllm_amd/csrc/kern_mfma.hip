@@ -17,6 +17,8 @@ __global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4))
 void k_mfma_dec(DecArgs A) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
     const int item = blockIdx.x / A.wgs;
+    if (A.n_items_dev && item >= *A.n_items_dev)
+        return;  // past the device planner's item count (the whole workgroup)
     dec_task<FMT, DUAL, TERMS, KS, NT, SR, PACK>(A, item, blockIdx.x - item * A.wgs,
                                                  (int)threadIdx.x, smem);
 }
@@ -175,12 +177,13 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
                            const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
-                           const DecDescK *inl) {
+                           const DecDescK *inl, const int *n_items_dev) {
     if (n_items <= 0)
         return n_cp > 0 ? hipErrorInvalidValue : hipSuccess;
-    if (K > kDecMaxK)
+    if (K > kDecMaxK || (n_items_dev && (inl || n_cp > 0)))
         return hipErrorInvalidValue;
     DecArgs a{};
+    a.n_items_dev = n_items_dev;
     a.desc = desc;
     a.xin = xin;
     a.pin = static_cast<const __bf16 *>(pin);

@@ -1,6 +1,7 @@
 // kern_misc.hip -- top-k combine and MXFP4 activation quantization for gfx950.
 #include "moe_internal.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace mvllm_hip {
@@ -59,6 +60,41 @@ hipError_t launch_combine(const CombineArgs &a, hipStream_t st) {
         return hipSuccess;
     const dim3 grid((unsigned)((a.D + 255) / 256), (unsigned)a.n_tok), block(64);
     hipLaunchKernelGGL(k_combine, grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+// n 8-byte words from pinned host memory (read over PCIe by the kernel) to device memory:
+// a small host-to-device copy that stays a kernel in the stream's queue.
+__global__ __launch_bounds__(256) void k_copy_words(const unsigned long long *src,
+                                                    unsigned long long *dst, int n) {
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+        dst[i] = src[i];
+}
+
+// Up to kArgWords 8-byte words carried in the kernel arguments (which the runtime places
+// in device memory): no host memory read at all.
+__global__ __launch_bounds__(256) void k_fill_words(ArgWords w, unsigned long long *dst) {
+    for (int i = threadIdx.x; i < w.n; i += 256)
+        dst[i] = w.v[i];
+}
+
+hipError_t launch_fill_words(const ArgWords &w, void *dst, hipStream_t st) {
+    if (w.n <= 0)
+        return hipSuccess;
+    if (w.n > kArgWords)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_fill_words, dim3(1), dim3(256), 0, st, w,
+                       static_cast<unsigned long long *>(dst));
+    return hipGetLastError();
+}
+
+hipError_t launch_copy_words(const void *host_src, void *dst, int n, hipStream_t st) {
+    if (n <= 0)
+        return hipSuccess;
+    const unsigned grid = (unsigned)std::min(32, (n + 255) / 256);
+    hipLaunchKernelGGL(k_copy_words, dim3(grid), dim3(256), 0, st,
+                       static_cast<const unsigned long long *>(host_src),
+                       static_cast<unsigned long long *>(dst), n);
     return hipGetLastError();
 }
 

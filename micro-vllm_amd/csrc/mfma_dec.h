@@ -60,7 +60,8 @@ struct DecArgs {
     __bf16 *pout;         // dual: H planes [TERMS][rcap][O]
     float *hp;            // dual, fmt 4: H partial sums [O/64][4][rcap]
     float *out;           // single: Y [rcap][O] f32, or the caller's out [S][O] with fold
-    int fold;             // single: add wts[r] * y into out[rows[r]] (float atomics)
+    int fold;             // single: add wts[r] * y into out[rows[r]] (float atomics); rows
+                          // with rows[r] < 0 are skipped
     // dual: workgroups [0, n_cp) copy descriptor i of cp_src (the down launch's, in host
     // memory) to cp_dst (device memory): the down kernel then starts from an HBM/L2 read
     // instead of a PCIe round trip (measured 20.6 -> 18.4 us at c1 T=16)
@@ -68,6 +69,9 @@ struct DecArgs {
     DecDesc *cp_dst;
     int n_cp;
     int pack;  // every item has <= 8 rows and TERMS == 2: the packed kernel is launched
+    // item count in device memory (a device planner's), or null: the grid then covers a
+    // capacity of items and the workgroups of items at or past the count return at once
+    const int *n_items_dev;
     int wgs;              // workgroups per item
     int K, O, rcap, rmax;
     int act;
@@ -680,7 +684,7 @@ __device__ __forceinline__ void dec_task(const DecArgs &A, int item, int wg, int
             const int tok = 4 * q + i;
             const int drow = (int)drow4[i];
             const float dwt = dwt4[i];
-            if (tok < nrow) {
+            if (tok < nrow && (!A.fold || drow >= 0)) {
 #pragma unroll
                 for (int n = 0; n < NT; ++n) {
                     const int o = tile[n] * 16 + t;

@@ -50,6 +50,15 @@ enum : int { ACT_SILU = 0, ACT_CLAMP_SWIGLU = 1, ACT_SITU = 2 };
 // Generic GEMV: any K, any alignment, fmt 0/4/7 (exact reference per-element formula).
 hipError_t launch_gemv_generic(int fmt, bool dual, const GemvArgs &a, hipStream_t st);
 hipError_t launch_combine(const CombineArgs &a, hipStream_t st);
+// n 8-byte words from pinned host memory to device memory by a kernel on st.
+hipError_t launch_copy_words(const void *host_src, void *dst, int n, hipStream_t st);
+// n <= kArgWords words in the kernel arguments, written to dst by a kernel on st.
+constexpr int kArgWords = 448;
+struct ArgWords {
+    unsigned long long v[kArgWords];
+    int n;
+};
+hipError_t launch_fill_words(const ArgWords &w, void *dst, hipStream_t st);
 hipError_t launch_dequant(int fmt, const void *packed, const void *scales, int O, int K,
                           float *w, hipStream_t st);
 hipError_t launch_dequant_bf16path(int fmt, const void *packed, const void *scales, int O,
@@ -135,12 +144,14 @@ inline int dec_max_kr(int fmt) { return fmt == 4 ? 2048 : 4096; }
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt);
 // inl (dual only, optional): the n_items (<= kDecInline) descriptors in the compact form,
 // in host memory; copied into the kernel arguments, and desc is not read.
+// n_items_dev (optional, not with inl or n_cp): the item count in device memory; n_items
+// is then the capacity the grid covers.
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
                            const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
-                           const DecDescK *inl = nullptr);
+                           const DecDescK *inl = nullptr, const int *n_items_dev = nullptr);
 
 // Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
 // nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per
@@ -260,7 +271,26 @@ struct CsrArgs {
     float *ent_w;  // [cap_rows]
 };
 
+// The decode-kernel plan of such a call (k_dplan_dec): per segment of live expert, items
+// of up to rmax rows with a gate/up and a down descriptor each.
+struct DPlanDecArgs {
+    const void *const *table;
+    int n_table;
+    long long off[6];
+    const int *counts, *eids, *xoff, *nr;
+    const int *rows;     // [cap_rows] out row of each compact row
+    const float *rw;     // [cap_rows] combine weights
+    int cap_e, cap_rows, S;
+    int rmax;            // rows per item (1..16)
+    int cap_items;       // descriptors the buffers hold (a bound for any valid input)
+    DecDesc *gu, *dn;    // [cap_items] each
+    int *n_items;        // [1]
+    unsigned char *row_ok;  // [cap_rows] (for the ordered combine's lists)
+    int *err;            // as DPlanArgs::err
+};
+
 hipError_t launch_dplan(const DPlanArgs &a, hipStream_t st);
+hipError_t launch_dplan_dec(const DPlanDecArgs &a, hipStream_t st);
 hipError_t launch_dcsr(const CsrArgs &a, hipStream_t st);
 
 }  // namespace mvllm_hip

@@ -270,13 +270,16 @@ struct Ctx {
     // unrecorded: the blocks are recycled when the last open table is closed)
     std::unordered_map<int, int> layer_open;
     std::unordered_map<int, std::vector<std::pair<size_t, void *>>> layer_parked;
-    // pinned staging of tier tables, a ring guarded by one event per entry
+    // pinned staging of tier tables of more than kArgWords entries, a ring guarded by one
+    // event per entry
     static constexpr int kTabSlots = 8, kTabMax = 8192;
     HostBuf tab_host[kTabSlots];
     hipEvent_t tab_done[kTabSlots] = {};
     bool tab_used[kTabSlots] = {};
     int tab_next = 0;
     hipEvent_t tier_ready = nullptr;  // copy stream: every promotion enqueued so far
+    // copies enqueued on the copy stream so far, and as of tier_ready's last record
+    unsigned long long copy_epoch = 0, tier_epoch = 0;
     std::vector<std::pair<size_t, void *>> pending_free;
     // stats
     double stats[20] = {0};
@@ -448,27 +451,18 @@ int pick_rmax(int fmt, int K, int O, int terms, bool dual, int want) {
     return 0;
 }
 
-bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t split, int fmt,
-               int K, int O, bool dual) {
-    // LDS holds activations for the largest item actually present, within the limits
-    int most = 1;
-    for (const ExpertWork &w : P.ew)
-        most = std::max(most, w.nrows);
-    ph.rmax = pick_rmax(fmt, K, O, cc.terms, dual, most);
-    if (ph.rmax < 1)
-        return false;
-    size_t n_items = 0;
-    for (const ExpertWork &w : P.ew)
-        n_items += (size_t)((w.nrows + ph.rmax - 1) / ph.rmax);
-    // Each wave streams nt tiles x K/ks.  Cost of an admissible (ks, nt): the busiest of
-    // the 256 CUs runs n = ceil(workgroups / 256) workgroups, each its waves' blocks plus a
-    // ramp of ~4 blocks; two workgroups sharing a CU overlap by ~15 %.  Ties keep the
-    // smaller split.  This picks the fastest choice measured on MI355X at c1 T = 1, 2, 4, 8
-    // and 16 and at c2, for both projections.
+// The (ks, nt) of a decode phase of n_items items of up to rmax rows; false if none fits.
+// Each wave streams nt tiles x K/ks.  Cost of an admissible (ks, nt): the busiest of
+// the 256 CUs runs n = ceil(workgroups / 256) workgroups, each its waves' blocks plus a
+// ramp of ~4 blocks; two workgroups sharing a CU overlap by ~15 %.  Ties keep the
+// smaller split.  This picks the fastest choice measured on MI355X at c1 T = 1, 2, 4, 8
+// and 16 and at c2, for both projections.
+bool pick_kt(const Ctx &C, int fmt, int K, int O, int rmax, int terms, bool dual,
+             size_t n_items, PhaseCfg &ph) {
     const size_t tiles = n_items * (size_t)(O / 16) * (dual ? 2 : 1);  // 16-row weight tiles
     double best = 1e30;
     for (const auto &kt : kDecOpts[dual ? 1 : 0]) {
-        if (!kt[0] || !dec_fits(fmt, K, O, ph.rmax, cc.terms, dual, kt[0], kt[1]))
+        if (!kt[0] || !dec_fits(fmt, K, O, rmax, terms, dual, kt[0], kt[1]))
             continue;
         if (C.dec_ks && kt[0] != C.dec_ks)
             continue;
@@ -482,7 +476,23 @@ bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t sp
             ph.nt = kt[1];
         }
     }
-    if (best >= 1e30)
+    ph.rmax = rmax;
+    return best < 1e30;
+}
+
+bool add_phase(const Ctx &C, CallCfg &cc, PhaseCfg &ph, const Plan &P, size_t split, int fmt,
+               int K, int O, bool dual) {
+    // LDS holds activations for the largest item actually present, within the limits
+    int most = 1;
+    for (const ExpertWork &w : P.ew)
+        most = std::max(most, w.nrows);
+    const int rmax = pick_rmax(fmt, K, O, cc.terms, dual, most);
+    if (rmax < 1)
+        return false;
+    size_t n_items = 0;
+    for (const ExpertWork &w : P.ew)
+        n_items += (size_t)((w.nrows + rmax - 1) / rmax);
+    if (!pick_kt(C, fmt, K, O, rmax, cc.terms, dual, n_items, ph))
         return false;
     ph.it0 = cc.items.size() / 4;
     ph.it_split = ph.it0;
@@ -1639,6 +1649,7 @@ int mvllm_hip_moe_block(int nb, int D, int Iinter, int fmt, int qgs, const void 
                 }
             }
         }
+        C.copy_epoch += 1;
         // one event for every call: a wait takes the record current when it is enqueued
         miss_ev = C.miss_done;
         HIP_TRY(hipEventRecord(miss_ev, C.copy));
@@ -1784,6 +1795,7 @@ int promote_locked(Ctx &C, const void *host_blob, size_t bytes, int layer, int e
     HIP_TRY(hipEventCreateWithFlags(&r.ready, hipEventDisableTiming));
     HIP_TRY(hipEventCreateWithFlags(&r.last_use, hipEventDisableTiming));
     HIP_TRY(hipMemcpyAsync(dev, host_blob, bytes, hipMemcpyHostToDevice, C.copy));
+    C.copy_epoch += 1;
     HIP_TRY(hipEventRecord(r.ready, C.copy));
     C.lru.push_front(key);
     r.lru = C.lru.begin();
@@ -1793,6 +1805,112 @@ int promote_locked(Ctx &C, const void *host_blob, size_t bytes, int layer, int e
     C.stats[5] += 1;
     C.stats[2] += static_cast<double>(bytes);
     *staged = 1;
+    return 1;
+}
+
+// mvllm_hip_moe_block_routed_dev at decode shapes (S <= 16 out rows): the decode kernels
+// on descriptors the device planner writes (k_dplan_dec), the top-k combine folded into
+// the down kernel as in the host-planned decode call, or with option combine_ordered the
+// ordered combine on device-built lists.  Three launches (five ordered) where the
+// grouped-GEMM path takes fifteen.  Returns -1 when the shapes do not take this path (the
+// caller runs the grouped GEMM), else the entry's result.  Arguments validated by the
+// caller, which holds C.mu.
+int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_table,
+               const int *counts, const int *eids, const int *xoff, const int *nr,
+               int cap_experts, const int *rows, const float *rw, int cap_rows, const float *x,
+               float *out, int S, int act, float act_a, float act_b, int *status,
+               hipStream_t st, const long long off6[6]) {
+    const int terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
+    if (C.gemm == 1 || S > 16 || D > kDecMaxK || I > kDecMaxK)
+        return -1;
+    for (int k = 0; k < 6; ++k)  // weights 16-byte aligned, scales 16 (int4) or 8 (MXFP4)
+        if (off6[k] % ((k & 1) && fmt == 7 ? 8 : 16))
+            return -1;
+    // rows per item: S, since a token picks an expert at most once, so no segment of
+    // routing output holds more rows (longer segments split into items of S rows).  Items
+    // at most: M segments of one item, plus one more per further S rows of the call
+    const int rmax = S;
+    const int M = std::min(cap_experts, cap_rows);
+    const int cap_items = M + (cap_rows - M) / rmax;
+    PhaseCfg gu, dn;
+    if (!pick_kt(C, fmt, D, I, rmax, terms, true, (size_t)cap_items, gu) ||
+        !pick_kt(C, fmt, I, D, rmax, terms, false, (size_t)cap_items, dn))
+        return -1;
+    const bool fold = !C.combine_ordered;
+    const bool pk = terms == 2 && rmax <= 8;  // the packed kernels (both terms in one MFMA)
+    auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
+    const size_t b_desc = al((size_t)cap_items * sizeof(DecDesc));
+    const size_t b_misc = 256, b_ok = al((size_t)cap_rows), b_cnt = al(((size_t)S + 1) * 4);
+    const size_t b_cur = al((size_t)S * 4), b_er = al((size_t)cap_rows * 4);
+    if (!order_after_previous(C, st))
+        return 0;
+    HIP_TRY(C.Rp.ensure(2 * b_desc + b_misc + b_ok + b_cnt + b_cur + 2 * b_er));
+    HIP_TRY(C.Ph.ensure((size_t)terms * cap_rows * I * 2));
+    if (fmt == 4)
+        HIP_TRY(C.HP.ensure((size_t)(I / 64) * 4 * cap_rows * 4));
+    if (!fold)
+        HIP_TRY(C.Y.ensure((size_t)cap_rows * D * 4));
+    char *p = static_cast<char *>(C.Rp.p);
+    DPlanDecArgs a{};
+    a.table = table;
+    a.n_table = n_table;
+    for (int k = 0; k < 6; ++k)
+        a.off[k] = off6[k];
+    a.counts = counts;
+    a.eids = eids;
+    a.xoff = xoff;
+    a.nr = nr;
+    a.rows = rows;
+    a.rw = rw;
+    a.cap_e = cap_experts;
+    a.cap_rows = cap_rows;
+    a.S = S;
+    a.rmax = rmax;
+    a.cap_items = cap_items;
+    a.gu = reinterpret_cast<DecDesc *>(p);
+    a.dn = reinterpret_cast<DecDesc *>(p + b_desc);
+    char *misc = p + 2 * b_desc;
+    a.n_items = reinterpret_cast<int *>(misc);
+    a.err = status ? status : reinterpret_cast<int *>(misc + 64);
+    a.row_ok = reinterpret_cast<unsigned char *>(misc + b_misc);
+    HIP_TRY(launch_dplan_dec(a, st));
+    float *hp = fmt == 4 ? static_cast<float *>(C.HP.p) : nullptr;
+    HIP_TRY(launch_mfma_dec(fmt, true, terms, gu.ks, gu.nt, a.gu, cap_items, x, nullptr, nullptr,
+                            C.Ph.p, hp, nullptr, D, I, cap_rows, rmax, act, act_a, act_b, false,
+                            pk, nullptr, nullptr, 0, st, nullptr, a.n_items));
+    HIP_TRY(launch_mfma_dec(fmt, false, terms, dn.ks, dn.nt, a.dn, cap_items, nullptr, C.Ph.p, hp,
+                            nullptr, nullptr, fold ? out : static_cast<float *>(C.Y.p), I, D,
+                            cap_rows, rmax, 0, 0.f, 0.f, fold, pk, nullptr, nullptr, 0, st,
+                            nullptr, a.n_items));
+    if (!fold) {
+        CsrArgs cs{};
+        cs.counts = counts;
+        cs.cap_rows = cap_rows;
+        cs.S = S;
+        cs.rows = rows;
+        cs.rw = rw;
+        cs.row_ok = a.row_ok;
+        cs.cnt = reinterpret_cast<int *>(misc + b_misc + b_ok);
+        cs.cursor = reinterpret_cast<int *>(misc + b_misc + b_ok + b_cnt);
+        cs.ent_row = reinterpret_cast<int *>(misc + b_misc + b_ok + b_cnt + b_cur);
+        cs.ent_w = reinterpret_cast<float *>(misc + b_misc + b_ok + b_cnt + b_cur + b_er);
+        HIP_TRY(launch_dcsr(cs, st));
+        CombineArgs cb{};
+        cb.Y = static_cast<const float *>(C.Y.p);
+        cb.tok_ptr = cs.cnt;
+        cb.ent_row = cs.ent_row;
+        cb.ent_w = cs.ent_w;
+        cb.out_row = nullptr;
+        cb.out = out;
+        cb.n_tok = S;
+        cb.D = D;
+        HIP_TRY(launch_combine(cb, st));
+    }
+    C.stats[0] += 1;
+    C.stats[13] += 1;
+    C.stats[14] += 1;
+    C.last_stream = st;
+    C.have_last = true;
     return 1;
 }
 
@@ -1887,11 +2005,17 @@ int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resi
         return 0;
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
+    // tables of up to kArgWords entries travel in a kernel's arguments; larger ones through
+    // a ring of pinned slots that a kernel reads, each slot guarded by an event
+    const bool in_args = n_experts <= kArgWords;
+    ArgWords aw;
     const int si = C.tab_next;
-    C.tab_next = (si + 1) % Ctx::kTabSlots;
-    if (C.tab_used[si])
-        HIP_TRY(hipEventSynchronize(C.tab_done[si]));
-    void **h = static_cast<void **>(C.tab_host[si].p);
+    if (!in_args) {
+        C.tab_next = (si + 1) % Ctx::kTabSlots;
+        if (C.tab_used[si])
+            HIP_TRY(hipEventSynchronize(C.tab_done[si]));
+    }
+    void **h = in_args ? reinterpret_cast<void **>(aw.v) : static_cast<void **>(C.tab_host[si].p);
     int count = 0;
     for (int e = 0; e < n_experts; ++e) {
         auto it = C.res.find(res_key(layer, e));
@@ -1901,13 +2025,27 @@ int mvllm_hip_tier_table(int layer, int n_experts, void **table_dev, int *n_resi
             ++count;
         }
     }
-    // the compute that reads the table runs after every promotion enqueued so far
-    HIP_TRY(hipEventRecord(C.tier_ready, C.copy));
-    HIP_TRY(hipStreamWaitEvent(st, C.tier_ready, 0));
-    HIP_TRY(hipMemcpyAsync(table_dev, h, (size_t)n_experts * sizeof(void *),
-                           hipMemcpyHostToDevice, st));
-    HIP_TRY(hipEventRecord(C.tab_done[si], st));
-    C.tab_used[si] = true;
+    // the compute that reads the table runs after every promotion enqueued so far: a wait
+    // unless those copies have all finished (a wait is a queue packet that idles the GPU)
+    if (C.tier_epoch != C.copy_epoch) {
+        HIP_TRY(hipEventRecord(C.tier_ready, C.copy));
+        C.tier_epoch = C.copy_epoch;
+    }
+    const hipError_t q = hipEventQuery(C.tier_ready);
+    if (q == hipErrorNotReady)
+        HIP_TRY(hipStreamWaitEvent(st, C.tier_ready, 0));
+    else
+        HIP_TRY(q);
+    // the table by a kernel (an asynchronous copy of a few KB idled the stream ~15 us per
+    // table; a kernel reading a pinned slot takes ~3.6 us, plus the slot's event)
+    if (in_args) {
+        aw.n = n_experts;
+        HIP_TRY(launch_fill_words(aw, table_dev, st));
+    } else {
+        HIP_TRY(launch_copy_words(h, table_dev, n_experts, st));
+        HIP_TRY(hipEventRecord(C.tab_done[si], st));
+        C.tab_used[si] = true;
+    }
     C.layer_open[layer] += 1;
     if (n_resident)
         *n_resident = count;
@@ -2083,6 +2221,13 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
         return 0;
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
+    long long off6[6];
+    (void)mvllm_expert_geom(fmt, D, Iinter, off6);
+    const int rd = routed_dec(C, D, Iinter, fmt, table, n_table, counts, eids, xoff, nr,
+                              cap_experts, rows, rw, cap_rows, x, out, S, act, act_a, act_b,
+                              status, st, off6);
+    if (rd >= 0)
+        return rd;
     // bf16 terms per activation: two (2^-17 relative, the decode accuracy) for calls of at
     // most 256 rows, one (the prefill arithmetic) above; mode 1 always two, mode 2 one
     const int terms = C.mode == 1 ? 2 : C.mode == 2 ? 1 : (cap_rows <= 256 ? 2 : 1);
@@ -2098,8 +2243,6 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
         base[c] = n_it;
         n_it += cap[c];
     }
-    long long off6[6];
-    (void)mvllm_expert_geom(fmt, D, Iinter, off6);
     auto al = [](size_t n) { return (n + 255) & ~size_t(255); };
     const size_t b_ew = al((size_t)cap_experts * sizeof(ExpertWork)), b_it = al((size_t)n_it * 16);
     const size_t b_misc = 256, b_ok = al((size_t)cap_rows), b_cnt = al(((size_t)S + 1) * 4);

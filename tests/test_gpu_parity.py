@@ -397,6 +397,43 @@ def test_config_parity(hip, orc, name, T):
 
 # ------------------------------------------------------------- residency / staging
 
+@pytest.mark.parametrize("n_experts", [300, 600])
+def test_tier_table_entries(hip, n_experts):
+    """mvllm_hip_tier_table writes each expert's HBM copy address (resident_ptr) or null,
+    for tables in a kernel's arguments (<= 448 entries) and through the pinned ring
+    (larger), the ring wrapped around more than once."""
+    L = hip.lib()
+    nbytes = 4096
+    layer = 40 + n_experts  # a layer no other test uses
+    eids = [0, 7, n_experts // 2 + 1, n_experts - 1]
+    blobs = []
+    for i, e in enumerate(eids):
+        p = L.mvllm_hip_host_alloc(nbytes)
+        assert p
+        ctypes.memset(p, i + 1, nbytes)
+        blobs.append(p)
+        hip.promote(p, nbytes, layer, e)
+    torch.cuda.synchronize()
+    try:
+        want = np.zeros(n_experts, np.uint64)
+        for e in eids:
+            want[e] = L.mvllm_hip_resident_ptr(layer, e)
+            assert want[e]
+        tab = torch.full((n_experts,), -1, dtype=torch.int64, device="cuda")
+        for rep in range(11):  # more calls than the ring has slots
+            tab.fill_(-1)
+            assert hip.tier_table(layer, n_experts, tab) == len(eids)
+            hip.tier_table_done(layer)
+            got = tab.cpu().numpy().view(np.uint64)
+            assert np.array_equal(got, want), rep
+    finally:
+        for e in eids:
+            hip.evict(layer, e)
+        torch.cuda.synchronize()
+        for p in blobs:
+            L.mvllm_hip_host_free(p)
+
+
 def test_promote_hits_and_evict(hip, orc):
     from mvllm_hip import synth
     say("promote")

@@ -2,13 +2,19 @@
 the block on the segments where the routing left them, experts resolved through a device
 blob table; no host round trip (src/model/glm53.cpp:1938-1992 with the device route).
 
-Checked against
+Two paths: calls of at most 16 out rows run the decode kernels on descriptors the device
+planner writes, others the grouped GEMM.  Checked against
   * the host-planned call on the same segments (read back) with the same arithmetic
-    (grouped GEMM, same bf16 terms): bit for bit, since items compute rows independently
-    and both combines sum in the reference's expert order;
+    (grouped GEMM and same bf16 terms; or the decode kernels with the same K split, the
+    same packed or unpacked form and the ordered combine on both sides): bit for bit,
+    since items compute rows independently and both combines sum in the reference's
+    expert order (decode calls of 9-16 out rows, packed on one side only: within 2e-6);
   * the oracle's host chain (moe_topk per token, moe_segments, moe_block) within the
     arithmetic's bar: 2e-5 for two bf16 terms per activation, 1e-2 (the north-star bar for
-    bf16 outputs) for one.
+    bf16 outputs) for one;
+  * the oracle's moe_block on hand-made segments the decode path must split (more rows
+    than out rows) and rows whose out row is out of range (skipped), with the combine
+    folded into the down kernel (float atomics) and ordered.
 Also: null and out-of-table experts consume their rows without writing, and calls whose
 caps exceed the routed sizes (surplus workgroups exit) give the same bits.
 """
@@ -112,38 +118,64 @@ def oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, act, 
 
 
 CASES = [
-    # fmt, D, I, T, E, k, routing
-    (7, 1024, 512, 6, 48, 4, "uniform"),      # decode-like: <= 256 rows, two terms
-    (4, 512, 256, 16, 64, 8, "uniform"),
-    (7, 512, 256, 300, 64, 8, "skewed"),      # > 256 rows: one term; hot experts of many rows
+    # fmt, D, I, T, E, k, routing, path
+    (7, 1024, 512, 6, 48, 4, "uniform", "decode"),   # <= 16 out rows: the decode kernels
+    (4, 1024, 512, 16, 64, 8, "uniform", "decode"),
+    (4, 512, 256, 16, 64, 8, "uniform", "gemm"),     # down K = 256: no decode kernel fits
+    (7, 512, 256, 300, 64, 8, "skewed", "gemm"),     # > 256 rows: one term; hot experts
 ]
+
+
+def set_options(hip, **kv):
+    for key, v in kv.items():
+        hip.set_option(key, v)
 
 
 @pytest.mark.parametrize("case", CASES)
 def test_routed_block(hip, orc, case):
-    fmt, D, I, T, E, k, routing = case
+    fmt, D, I, T, E, k, routing, path = case
     say("routed block", case)
     from mvllm_hip import ACT_CLAMP_SWIGLU, ACT_SITU
     act, a, b = (ACT_CLAMP_SWIGLU, 7.0, 0.0) if fmt == 4 else (ACT_SITU, 4.0, 25.0)
     rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 17 + T,
                                                           routing=routing)
     seg = route(hip, choice, mix, k)
-    got, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)
+    got, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)  # default options
     assert status == 0
     two_terms = T * k <= 256
-    # the host-planned call with the same arithmetic: grouped GEMM, same terms
-    hip.set_option("gemm", 1)
-    hip.set_option("mode", 1 if two_terms else 0)
-    try:
-        ref, info = host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, act, a, b, table)
-    finally:
-        hip.set_option("gemm", 0)
-        hip.set_option("mode", 0)
+    if path == "decode":
+        # both sides: the decode kernels with one K split, the ordered combine
+        set_options(hip, dec_ks=2, combine_ordered=1)
+        try:
+            got_o, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)
+            ref, info = host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, act, a, b,
+                                     table)
+        finally:
+            set_options(hip, dec_ks=0, combine_ordered=0)
+        assert status == 0
+        if T <= 8:  # both sides run the packed kernels (items of <= 8 rows)
+            assert np.array_equal(got_o.view(np.uint32), ref.view(np.uint32))
+        else:  # the routed side's items hold up to T rows: the unpacked kernels
+            say("  vs host-planned decode: rel", npref.rel_err(got_o, ref))
+            assert npref.rel_err(got_o, ref) < 2e-6
+        # the default call: its own K split and the folded combine (float atomics, any
+        # expert order): the same arithmetic up to summation order
+        say("  default vs ordered, split 2: rel", npref.rel_err(got, got_o))
+        assert npref.rel_err(got, got_o) < 1e-5
+    else:
+        # the host-planned call with the same arithmetic: grouped GEMM, same terms
+        set_options(hip, gemm=1, mode=1 if two_terms else 0)
+        try:
+            ref, info = host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, act, a, b,
+                                     table)
+        finally:
+            set_options(hip, gemm=0, mode=0)
     nb, _, _, g_nr, _, _ = info
     say(f"  segments {nb}, rows {int(g_nr.sum())}, largest {int(g_nr.max())}")
     if routing == "skewed":
         assert int(g_nr.max()) > 64  # the top row class runs
-    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    if path == "gemm":
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     exp = oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, act, a, b)
     err = npref.rel_err(got, exp)
     say("  rel_err vs oracle chain", err)
@@ -185,4 +217,62 @@ def test_routed_block_surplus_caps(hip):
     b = run_routed(hip, fmt, D, I, table, route(hip, choice, mix, k, cap_rows=T * k + 200,
                                                 cap_e=E + 50), X, T, ACT_CLAMP_SWIGLU, 7.0,
                    0.0)[0]
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("ordered", [0, 1])
+def test_routed_decode_split_rows_and_dead_rows(hip, orc, ordered):
+    """Hand-made segments on the decode path (S = 4 out rows): segments of 6 and 9 rows
+    (more than S: split into items of S rows), rows whose out row is -1 or S (skipped), a
+    repeated out row within a segment, and an out-of-table expert; against the oracle's
+    moe_block on the same segments."""
+    from mvllm_hip import ACT_SITU, synth
+    fmt, D, I, S, E = 7, 512, 512, 4, 16
+    rng, pool, stride, geom, X, _, _, table = layer(hip, fmt, D, I, S, E, 2, 404)
+    eids = np.array([3, 7, 40, 11], np.int32)   # 40: outside the table
+    nr = np.array([6, 9, 2, 3], np.int32)
+    xoff = np.concatenate([[0], np.cumsum(nr)[:-1]]).astype(np.int32)
+    n = int(nr.sum())
+    rows = rng.integers(0, S, n).astype(np.int32)
+    rows[2], rows[8], rows[15] = -1, S, -3   # dead rows
+    rows[9] = rows[10]                       # one out row twice in a segment
+    rw = rng.uniform(0.1, 1.0, n).astype(np.float32)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    seg = (torch.tensor([len(eids), n], **i32), dev(eids), dev(xoff), dev(nr), dev(rows),
+           dev(rw))
+    set_options(hip, combine_ordered=ordered)
+    try:
+        got, status = run_routed(hip, fmt, D, I, table, seg, X, S, ACT_SITU, 4.0, 25.0)
+    finally:
+        set_options(hip, combine_ordered=0)
+    assert status == 0
+    lists = [[], [], [], [], [], []]
+    for e in eids:
+        pieces = synth.blob_pieces(pool[int(e)].cpu().numpy(), fmt, D, I, geom[1]) \
+            if e < E else [None] * 6
+        for j in range(6):
+            lists[j].append(pieces[j])
+    xg = X[np.clip(rows, 0, S - 1)]
+    exp = np.zeros((S, D), np.float32)
+    assert orc.moe_block(len(eids), D, I, fmt, *lists, xg, xoff, nr, rows, rw, exp, S,
+                         ACT_SITU, 4.0, 25.0) == 1
+    err = npref.rel_err(got, exp)
+    say(f"split / dead rows (ordered={ordered}): rel_err", err)
+    assert err < 2e-5
+
+
+def test_routed_decode_surplus_caps(hip):
+    """Decode path: caps above the routed sizes (grids sized for them, surplus workgroups
+    exit at the planner's item count) give the same bits as exact caps (ordered combine)."""
+    fmt, D, I, T, E, k = 7, 1024, 512, 8, 64, 8
+    from mvllm_hip import ACT_SITU
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 6)
+    set_options(hip, combine_ordered=1, dec_ks=2)
+    try:
+        a = run_routed(hip, fmt, D, I, table, route(hip, choice, mix, k), X, T, ACT_SITU, 4.0,
+                       25.0)[0]
+        b = run_routed(hip, fmt, D, I, table, route(hip, choice, mix, k, cap_rows=T * k + 200,
+                                                    cap_e=E + 50), X, T, ACT_SITU, 4.0, 25.0)[0]
+    finally:
+        set_options(hip, combine_ordered=0, dec_ks=0)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
