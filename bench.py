@@ -239,7 +239,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
-                    help="only the headline workload (profiling runs)")
+                    help="only the headline workload (profiling runs: no other workloads, "
+                         "no c4 hot-segment calls)")
     ap.add_argument("--probe-sizes", action="store_true",
                     help="also time the stream-read probe at launch-sized reads (8 MiB .. "
                          "1 GiB, each repetition at a new offset of the pool)")
@@ -298,7 +299,7 @@ def main():
     sizes = probe_sizes(np, mvllm_hip, pool.pool, sink, probe_bytes) if args.probe_sizes else {}
 
     extra = {}
-    if args.config == "c4":
+    if args.config == "c4" and not args.no_extra:  # (profiling runs: the call alone)
         hot = hot_segments(np, torch, mvllm_hip, w, pool, cfg, T, args.steps, 2)
         if hot:
             extra["c4 hot segments"] = hot
