@@ -178,7 +178,8 @@ def measure(np, torch, mvllm_hip, synth, name, T, steps, warmup, pool_gb, fp4act
     lb_gu = binding_roof_us(nr, b_gu, 4.0 * D * I, peak)
     lb_call = binding_roof_us(nr, b_gu + b_dn, 6.0 * D * I, peak)
     wl = f"{name} T={T}" + (" fp4act" if fp4act else "")
-    kern = ("k_gemm_fp4 + k_gemm gate/up" if fp4act else "k_gemm gate/up") if gemm else \
+    kern = ("k_gemm_fp4 + k_gemm gate/up" if fp4act else
+            "k_gemm + k_gemm_wide gate/up" if fmt == 7 else "k_gemm gate/up") if gemm else \
         "k_mfma_dec gate/up"
     rec = {
         "workload": f"{name} {cfg['desc']}, T={T}" + (", native MXFP4 activations" if fp4act else ""),
