@@ -304,6 +304,8 @@ def main():
         hot = hot_segments(np, torch, mvllm_hip, w, pool, cfg, T, args.steps, 2)
         if hot:
             extra["c4 hot segments"] = hot
+        extra["c4 routed_dev"] = routed_prefill(np, torch, mvllm_hip, w, pool, cfg, T,
+                                                args.steps, 2)
     if not args.no_extra:
         if args.config == "c4" and not args.fp4act:
             rec, _, _ = measure(np, torch, mvllm_hip, synth, "c4", T, args.steps, 2,
@@ -352,6 +354,63 @@ def main():
         "extra": extra,
     }
     print(json.dumps(rec), flush=True)
+
+
+def routed_prefill(np, torch, mvllm_hip, w, pool, cfg, T, steps, warmup):
+    """The device-resident block at the c4 shape: mvllm_hip_moe_block_routed_dev on the
+    workload's segments in device memory (as mvllm_hip_moe_route_dev leaves them) with a
+    device table of the pool layer's blobs, against the host-planned moe_block_dev call on
+    the same segments and the same rotation of pool layers (HIP events around `steps`
+    calls of each, after `warmup`).  Both write the same out rows; the routed call plans on
+    the device and launches its grids for the caps (cap_experts = E, cap_rows = T k)."""
+    D, I, fmt, E = cfg["D"], cfg["I"], cfg["fmt"], cfg["E"]
+    i32 = dict(dtype=torch.int32, device="cuda")
+    n_rows = int(np.sum(w.nr))
+    counts = torch.tensor([w.nb, n_rows], **i32)
+    eids = torch.from_numpy(np.ascontiguousarray(w.eids, np.int32)).cuda()
+    xoff = torch.from_numpy(np.ascontiguousarray(w.xoff, np.int32)).cuda()
+    nr = torch.from_numpy(np.ascontiguousarray(w.nr, np.int32)).cuda()
+    rows = torch.from_numpy(np.ascontiguousarray(w.rows, np.int32)).cuda()
+    rw = torch.from_numpy(np.ascontiguousarray(w.rw, np.float32)).cuda()
+    x = torch.from_numpy(np.ascontiguousarray(w.x, np.float32)).cuda()
+    xg = torch.from_numpy(w.xg).cuda()
+    out = torch.zeros((T, D), dtype=torch.float32, device="cuda")
+    b0 = pool.pool.data_ptr()
+    tables = []
+    for layer in range(pool.layers):
+        t = np.zeros(E, np.int64)
+        for i in range(w.nb):
+            t[int(w.eids[i])] = b0 + (layer * w.nb + i) * pool.stride
+        tables.append(torch.from_numpy(t).cuda())
+    status = torch.zeros(1, **i32)
+
+    def routed(s):
+        mvllm_hip.moe_block_routed_dev(D, I, fmt, tables[s % len(tables)], E, counts, eids, xoff,
+                                       nr, rows, rw, x, out, T, w.act, w.a, w.b, status=status)
+
+    def planned(s):
+        mvllm_hip.moe_block_dev(w.nb, D, I, fmt, None, None, None, None, None, None, xg,
+                                w.xoff, w.nr, w.rows, w.rw, out, T, w.act, w.a, w.b,
+                                prepared=pool.lists[s % pool.layers])
+
+    rec = {}
+    for key, fn in (("routed_dev_us", routed), ("host_planned_us", planned)):
+        for s in range(warmup):
+            fn(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(steps):
+            fn(s)
+        e1.record()
+        torch.cuda.synchronize()
+        rec[key] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
+    if int(status.cpu()[0]) != 0:
+        raise SystemExit("routed_dev reported status %d" % int(status.cpu()[0]))
+    rec["ratio"] = round(rec["routed_dev_us"] / rec["host_planned_us"], 4)
+    log(f"c4 device-resident block: {rec['routed_dev_us']:.1f} us per call, host-planned "
+        f"{rec['host_planned_us']:.1f} us ({rec['ratio']:.3f})")
+    return rec
 
 
 def hot_segments(np, torch, mvllm_hip, w, pool, cfg, T, steps, warmup, min_rows=332):

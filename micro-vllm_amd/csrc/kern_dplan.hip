@@ -29,6 +29,19 @@ __device__ __forceinline__ int dplan_class(int n) {
     return n <= 16 ? 0 : n <= 32 ? 1 : n <= 64 ? 2 : 3;
 }
 
+// Items per class of a segment of n live rows, the host planner's rule (plan_gemm): full
+// blocks of bm rows in the top class, the remainder in the smallest class that holds it,
+// or with split64 a remainder of 33-64 rows as two items of the 32-row class.
+__device__ __forceinline__ void dplan_counts(const DPlanArgs &A, int n, int (&k)[4]) {
+    k[0] = k[1] = k[2] = k[3] = 0;
+    k[A.top] = n / A.bm;
+    const int rem = n % A.bm;
+    if (rem && A.split64 && rem > 32 && rem <= 64)
+        k[1] += 2;
+    else if (rem)
+        k[dplan_class(rem)] += 1;
+}
+
 // The blob of expert e (null when e is outside the table, its entry is null or not
 // 256-byte aligned: err = 2 for the last) and the live row count of a segment at compact
 // row x0 with nr rows (out of nrows).
@@ -90,9 +103,11 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
             continue;
         for (int j = x0; j < x0 + n; ++j)
             A.row_ok[j] = 1;
-        cnt[A.top] += n / A.bm;
-        if (n % A.bm)
-            cnt[dplan_class(n % A.bm)] += 1;
+        int k[4];
+        dplan_counts(A, n, k);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            cnt[c] += k[c];
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c)
@@ -129,14 +144,33 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
     for (int i = s0; i < s1; ++i) {
         const ExpertWork &w = A.ew[i];
         const int n = w.nrows;
-        for (int r0 = 0; r0 < n; r0 += A.bm) {
-            const int nrow = min(A.bm, n - r0);
-            const int c = nrow == A.bm ? A.top : dplan_class(nrow);
+        // word 3: (index in the segment's run of items of the class << 16) | run length,
+        // as the host writes it (the 16- and 32-row kernels order a run's tasks column
+        // block by column block).  A run that would pass the class's capacity (inputs whose
+        // segments overlap) is written as items alone: a run's tasks index all its items,
+        // and those past the capacity are never written.
+        int k[4], idx[4] = {0, 0, 0, 0};
+        dplan_counts(A, n, k);
+        auto put = [&](int c, int r0, int nrow) {
+            const bool fits = pos[c] - idx[c] + k[c] <= A.item_cap[c];
+            const int word = k[c] < 0x8000 && fits ? (idx[c] << 16) | k[c] : 1;
+            ++idx[c];
             if (pos[c] < A.item_cap[c])
-                A.items[A.item_base[c] + pos[c]] = int4{i, r0, nrow, 0};
+                A.items[A.item_base[c] + pos[c]] = int4{i, r0, nrow, word};
             else
                 *A.err = 1;
             ++pos[c];
+        };
+        for (int r0 = 0; r0 < n; r0 += A.bm) {
+            const int nrow = min(A.bm, n - r0);
+            if (nrow == A.bm) {
+                put(A.top, r0, nrow);
+            } else if (A.split64 && nrow > 32 && nrow <= 64) {
+                put(1, r0, 32);
+                put(1, r0 + 32, nrow - 32);
+            } else {
+                put(dplan_class(nrow), r0, nrow);
+            }
         }
     }
     if (tid < 4)

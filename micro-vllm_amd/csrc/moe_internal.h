@@ -249,6 +249,7 @@ struct DPlanArgs {
     int cap_e, cap_rows;
     int bm;            // rows per full block (16 * top class)
     int top;           // index of the top class (log2 of its MT)
+    int split64;       // remainders of 33-64 rows as two items of the 32-row class
     ExpertWork *ew;    // [cap_e]
     int4 *items;       // class c at items + item_base[c] ({expert, r0, nrow, 0})
     int item_base[4], item_cap[4];

@@ -2233,13 +2233,20 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     const int terms = C.mode == 1 ? 2 : C.mode == 2 ? 1 : (cap_rows <= 256 ? 2 : 1);
     const int max_mt = gemm_max_mt(fmt, terms);
     const int top = max_mt == 8 ? 3 : 2, bm = 16 * max_mt;
+    // remainders of 33-64 rows as two 32-row items, as the host planner does (plan_gemm)
+    const bool split64 = terms == 1 && max_mt >= 4;
     // items per class at most: one remainder per expert of >= lo rows; the top class's
-    // items (full blocks and remainders above bm / 2) hold >= lo[top] rows each
+    // items (full blocks and remainders above bm / 2) hold >= lo[top] rows each; with
+    // split64 the 32-row class holds up to two items per expert, >= 16 rows per item
     static const int lo[4] = {1, 17, 33, 65};
     int cap[4] = {0, 0, 0, 0}, base[4] = {0, 0, 0, 0}, n_it = 0;
     for (int c = 0; c <= top; ++c) {
         if (cap_rows >= lo[c])
             cap[c] = c == top ? cap_rows / lo[c] : std::min(cap_experts, cap_rows / lo[c]);
+        if (split64 && c == 1)
+            cap[c] = std::min(2 * cap_experts, cap_rows / 16);
+        if (split64 && c == 2)
+            cap[c] = 0;
         base[c] = n_it;
         n_it += cap[c];
     }
@@ -2268,6 +2275,7 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     a.cap_rows = cap_rows;
     a.bm = bm;
     a.top = top;
+    a.split64 = split64 ? 1 : 0;
     a.ew = reinterpret_cast<ExpertWork *>(p);
     a.items = reinterpret_cast<int4 *>(p + b_ew);
     for (int c = 0; c < 4; ++c) {
