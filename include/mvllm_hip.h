@@ -205,7 +205,7 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
  * surplus workgroups exit.  Two paths:
  *   S <= 16 (decode): the decode kernels of mvllm_hip_moe_block_dev's decode-shaped calls
  *     (two bf16 terms per activation; mode 1 three, mode 2 one) on items of up to S rows
- *     of one expert, and, as there, the combine folded into the down kernel as float
+ *     of one expert (fewer where the activations of S rows do not fit the kernels), and, as there, the combine folded into the down kernel as float
  *     atomics (out row sums in any expert order) unless option combine_ordered is 1;
  *     three launches.  Option gemm=1 takes the grouped path instead.
  *   otherwise: the grouped GEMM with two bf16 terms per activation (2^-17) when cap_rows

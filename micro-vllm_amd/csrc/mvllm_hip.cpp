@@ -1826,10 +1826,14 @@ int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_ta
     for (int k = 0; k < 6; ++k)  // weights 16-byte aligned, scales 16 (int4) or 8 (MXFP4)
         if (off6[k] % ((k & 1) && fmt == 7 ? 8 : 16))
             return -1;
-    // rows per item: S, since a token picks an expert at most once, so no segment of
-    // routing output holds more rows (longer segments split into items of S rows).  Items
-    // at most: M segments of one item, plus one more per further S rows of the call
-    const int rmax = S;
+    // rows per item: S (a token picks an expert at most once, so no segment of routing
+    // output holds more rows), or fewer where the activations of S rows do not fit the
+    // kernels' staging; longer segments split into items of rmax rows.  Items at most: M
+    // segments of one item, plus one more per further rmax rows of the call
+    const int rmax = std::min(pick_rmax(fmt, D, I, terms, true, S),
+                              pick_rmax(fmt, I, D, terms, false, S));
+    if (rmax < 1)
+        return -1;
     const int M = std::min(cap_experts, cap_rows);
     const int cap_items = M + (cap_rows - M) / rmax;
     PhaseCfg gu, dn;

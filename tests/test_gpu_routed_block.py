@@ -121,6 +121,7 @@ CASES = [
     # fmt, D, I, T, E, k, routing, path
     (7, 1024, 512, 6, 48, 4, "uniform", "decode"),   # <= 16 out rows: the decode kernels
     (4, 1024, 512, 16, 64, 8, "uniform", "decode"),
+    (7, 4096, 512, 8, 64, 8, "uniform", "decode"),    # items of 4 rows: 8 rows do not fit
     (4, 512, 256, 16, 64, 8, "uniform", "gemm"),     # down K = 256: no decode kernel fits
     (7, 512, 256, 300, 64, 8, "skewed", "gemm"),     # > 256 rows: one term; hot experts
 ]
