@@ -1836,6 +1836,8 @@ int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_ta
         return -1;
     const int M = std::min(cap_experts, cap_rows);
     const int cap_items = M + (cap_rows - M) / rmax;
+    if (cap_items > 8192)  // caps far beyond a decode call's rows: the grouped path
+        return -1;
     PhaseCfg gu, dn;
     if (!pick_kt(C, fmt, D, I, rmax, terms, true, (size_t)cap_items, gu) ||
         !pick_kt(C, fmt, I, D, rmax, terms, false, (size_t)cap_items, dn))

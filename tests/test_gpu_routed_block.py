@@ -221,15 +221,19 @@ def test_routed_block_surplus_caps(hip):
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("ordered", [0, 1])
-def test_routed_decode_split_rows_and_dead_rows(hip, orc, ordered):
+@pytest.mark.parametrize("fmt,ordered,mode", [(7, 0, 0), (7, 1, 0), (4, 0, 0), (4, 1, 1),
+                                              (7, 0, 2)])
+def test_routed_decode_split_rows_and_dead_rows(hip, orc, fmt, ordered, mode):
     """Hand-made segments on the decode path (S = 4 out rows): segments of 6 and 9 rows
     (more than S: split into items of S rows), rows whose out row is -1 or S (skipped), a
     repeated out row within a segment, and an out-of-table expert; against the oracle's
-    moe_block on the same segments."""
-    from mvllm_hip import ACT_SITU, synth
-    fmt, D, I, S, E = 7, 512, 512, 4, 16
-    rng, pool, stride, geom, X, _, _, table = layer(hip, fmt, D, I, S, E, 2, 404)
+    moe_block on the same segments, with the folded and the ordered combine and each
+    activation arithmetic (mode 0: two bf16 terms, bar 2e-5; mode 1: three, exact
+    products, 2e-5; mode 2: one, the bf16 bar 1e-2)."""
+    from mvllm_hip import ACT_CLAMP_SWIGLU, ACT_SITU, synth
+    D, I, S, E = 512, 512, 4, 16
+    act, a, b = (ACT_CLAMP_SWIGLU, 7.0, 0.0) if fmt == 4 else (ACT_SITU, 4.0, 25.0)
+    rng, pool, stride, geom, X, _, _, table = layer(hip, fmt, D, I, S, E, 2, 404 + fmt)
     eids = np.array([3, 7, 40, 11], np.int32)   # 40: outside the table
     nr = np.array([6, 9, 2, 3], np.int32)
     xoff = np.concatenate([[0], np.cumsum(nr)[:-1]]).astype(np.int32)
@@ -241,11 +245,11 @@ def test_routed_decode_split_rows_and_dead_rows(hip, orc, ordered):
     i32 = dict(dtype=torch.int32, device="cuda")
     seg = (torch.tensor([len(eids), n], **i32), dev(eids), dev(xoff), dev(nr), dev(rows),
            dev(rw))
-    set_options(hip, combine_ordered=ordered)
+    set_options(hip, combine_ordered=ordered, mode=mode)
     try:
-        got, status = run_routed(hip, fmt, D, I, table, seg, X, S, ACT_SITU, 4.0, 25.0)
+        got, status = run_routed(hip, fmt, D, I, table, seg, X, S, act, a, b)
     finally:
-        set_options(hip, combine_ordered=0)
+        set_options(hip, combine_ordered=0, mode=0)
     assert status == 0
     lists = [[], [], [], [], [], []]
     for e in eids:
@@ -256,10 +260,10 @@ def test_routed_decode_split_rows_and_dead_rows(hip, orc, ordered):
     xg = X[np.clip(rows, 0, S - 1)]
     exp = np.zeros((S, D), np.float32)
     assert orc.moe_block(len(eids), D, I, fmt, *lists, xg, xoff, nr, rows, rw, exp, S,
-                         ACT_SITU, 4.0, 25.0) == 1
+                         act, a, b) == 1
     err = npref.rel_err(got, exp)
-    say(f"split / dead rows (ordered={ordered}): rel_err", err)
-    assert err < 2e-5
+    say(f"split / dead rows (fmt={fmt}, ordered={ordered}, mode={mode}): rel_err", err)
+    assert err < (1e-2 if mode == 2 else 2e-5)
 
 
 def test_routed_decode_surplus_caps(hip):
