@@ -9,7 +9,8 @@
 // output columns, NT / 2 of each).  K advances 256 per step:
 //   * A: the item's rows of the bf16 input planes go straight into LDS (buffer_load ...
 //     lds, double buffered, one step ahead); rows are 512 bytes apart and a row's 16-byte
-//     chunks are XOR-swizzled by the row's low four bits (conflict-free fragment reads);
+//     chunks are XOR-swizzled by a mask of the row's low four bits (wide_swz: conflict-free
+//     fragment reads);
 //   * weight scales: the step's 8 ue8m0 bytes of each of the workgroup's weight rows go
 //     into LDS the same way (4-byte loads), next to the A tile;
 //   * weights: each wave's tiles two steps ahead in registers.  Lane (t, q) of a tile
@@ -47,6 +48,13 @@ constexpr int kWideBK = 256;
 __host__ __device__ constexpr int wide_stage_bytes(int mt, int nt, int waves) {
     return 16 * mt * kWideBK * 2 + waves * nt * 16 * 8;
 }
+
+// XOR mask of a row's 16-byte chunks in LDS (t = the row's low four bits): 2 (t mod 8) +
+// t / 8.  With it the fragment reads (lane 16 q + t reads row t's chunk 4 q + s) run at
+// the LDS's full read rate in a microbenchmark of this access pattern; XOR by t itself
+// ran them 1.7 x slower (the kernel's time did not change: its LDS reads are not what
+// bounds it).
+__device__ __forceinline__ uint32_t wide_swz(uint32_t t) { return ((t & 7u) << 1) | (t >> 3); }
 
 template <bool DUAL, int MT, int NT, int WAVES>
 __global__ __launch_bounds__(64 * WAVES) void k_gemm_wide(WideArgs A) {
@@ -107,7 +115,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_wide(WideArgs A) {
 
     // A of step k into LDS buffer buf.  DMA load i of wave w fills the two rows
     // r0 = 16 (i / R) + 2 w + 2 WAVES (i % R) and r0 + 1 (R = 8 / WAVES; lane l: row r0 + l / 32,
-    // physical chunk l % 32, which holds logical chunk (l % 32) ^ (row % 16)).  A lane's
+    // physical chunk l % 32, which holds logical chunk (l % 32) ^ wide_swz(row % 16)).  A lane's
     // rows then share row % 16 across its loads, so its offsets differ by scalars only.
     // Rows past nrow lie beyond the buffer: zeros.
     constexpr int R = 8 / WAVES;
@@ -118,7 +126,8 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_wide(WideArgs A) {
     // offset comes from a captured array)
     auto va_of = [&](int j) {
         const int r = 2 * wave + 2 * WAVES * j + (lane >> 5);
-        return (uint32_t)r * (uint32_t)K * 2u + 16u * (uint32_t)((lane & 31) ^ (r & 15));
+        return (uint32_t)r * (uint32_t)K * 2u +
+               16u * ((uint32_t)(lane & 31) ^ wide_swz((uint32_t)(r & 15)));
     };
     const uint32_t va0 = va_of(0), va1 = R > 1 ? va_of(1) : 0u;
     auto dma_a = [&] __attribute__((always_inline)) (int k, int buf) {
@@ -158,7 +167,7 @@ __global__ __launch_bounds__(64 * WAVES) void k_gemm_wide(WideArgs A) {
 
     // LDS byte offsets of this lane: A row t's chunk for MFMA step s is
     // abase ^ (256 (s / 4) + 16 (s % 4)) (row tile mt: + mt 8192), its scales sbase (+ 128 m)
-    const uint32_t abase = (uint32_t)t * 512u + 16u * (uint32_t)((4 * q) ^ t);
+    const uint32_t abase = (uint32_t)t * 512u + 16u * ((uint32_t)(4 * q) ^ wide_swz((uint32_t)t));
     const uint32_t sbase = (uint32_t)ABYTES + ((uint32_t)wave * NT * 16u + (uint32_t)t) * 8u;
     // scales of the lane's block (q for h = 0, 4 + q for h = 1) of every tile
     auto read_sc = [&] __attribute__((always_inline)) (const char *base, int h, float (&sc)[NT]) {
