@@ -207,7 +207,7 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
  *     (two bf16 terms per activation; mode 1 three, mode 2 one) on items of up to S rows
  *     of one expert (fewer where the activations of S rows do not fit the kernels), and, as there, the combine folded into the down kernel as float
  *     atomics (out row sums in any expert order) unless option combine_ordered is 1;
- *     three launches.  Option gemm=1 takes the grouped path instead.
+ *     two launches (the gate/up kernel plans its own items).  Option gemm=1 takes the grouped path instead.
  *   otherwise: the grouped GEMM with two bf16 terms per activation (2^-17) when cap_rows
  *     <= 256, one above (mode option 1: always two, 2: always one), and the ordered
  *     combine on lists built by kernels.

@@ -33,6 +33,109 @@ void k_mfma_dec_inl(DecArgs A, DecInline I) {
                                                       (int)threadIdx.x, smem, I.d);
 }
 
+// Wave 0 of a k_mfma_dec_seg workgroup (lane 0..63): the descriptor of item `item` in kd
+// (kd->nrow = 0 when the call has no such item).  Items are the rmax-row pieces of the live
+// segments in segment order, k_dplan_dec's numbering: a segment whose expert id is outside
+// the table, or whose blob is null or not 256-byte aligned, or that has no rows, has none.
+// Column block 0 of each item also writes the item's down descriptor; workgroup 0 the
+// item count and the status.
+__device__ __forceinline__ void seg_plan(const DecSegArgs &G, int item, int wg, int lane,
+                                         DecDescK *kd) {
+    const int nb = min(max(G.counts[0], 0), G.cap_e);
+    const int nrows = min(max(G.counts[1], 0), G.cap_rows);
+    int base = 0, err = 0;
+    bool mine = false;
+    const char *my_blob = nullptr;
+    int my_x0 = 0, my_n = 0, my_r0 = 0;
+    for (int c0 = 0; c0 < nb; c0 += 64) {  // uniform trip count
+        const int i = c0 + lane;
+        int cnt = 0, x0 = 0, n = 0;
+        const char *blob = nullptr;
+        if (i < nb) {
+            const int e = G.eids[i];
+            x0 = G.xoff[i];
+            const int nri = G.nr[i];
+            n = (x0 < 0 || x0 > nrows) ? 0 : max(0, min(nri, nrows - max(x0, 0)));
+            blob = (e >= 0 && e < G.n_table) ? static_cast<const char *>(G.table[e]) : nullptr;
+            if (reinterpret_cast<uintptr_t>(blob) & 255) {
+                err = 2;
+                blob = nullptr;
+            }
+            cnt = (blob && n) ? (n + G.rmax - 1) / G.rmax : 0;
+        }
+        int incl = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (lane >= o)
+                incl += v;
+        }
+        const int excl = incl - cnt;
+        if (cnt && item >= base + excl && item < base + incl) {
+            mine = true;
+            my_blob = blob;
+            my_x0 = x0;
+            my_n = n;
+            my_r0 = (item - base - excl) * G.rmax;
+        }
+        base += __shfl(incl, 63);
+    }
+    if (item == 0 && wg == 0) {
+        const bool any_err = __builtin_amdgcn_ballot_w64(err != 0) != 0;
+        if (lane == 0) {
+            *G.n_items = min(base, G.cap_items);
+            *G.err = any_err ? 2 : 0;
+        }
+    }
+    if (__builtin_amdgcn_ballot_w64(mine) == 0 || item >= G.cap_items) {
+        if (lane == 0)
+            kd->nrow = 0;
+        return;
+    }
+    if (!mine)
+        return;
+    const int jb = my_x0 + my_r0, nrow = min(G.rmax, my_n - my_r0);
+    DecDescK k;
+    k.w0 = my_blob + G.off[0];
+    k.off[0] = (int)(G.off[2] - G.off[0]);
+    k.off[1] = (int)(G.off[1] - G.off[0]);
+    k.off[2] = (int)(G.off[3] - G.off[0]);
+    k.jbase = (unsigned short)jb;
+    k.nrow = (unsigned short)nrow;
+    DecDesc d{};
+    d.w[0] = d.w[1] = my_blob + G.off[4];
+    d.s[0] = d.s[1] = my_blob + G.off[5];
+    d.jbase = jb;
+    d.nrow = nrow;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int t = r < nrow ? G.rows[jb + r] : 0;
+        const bool ok = r < nrow && t >= 0 && t < G.S;
+        k.rows[r] = (unsigned short)(ok ? t : 0);
+        d.rows[r] = ok ? t : -1;
+        d.wts[r] = r < nrow ? G.rw[jb + r] : 0.f;
+    }
+    *kd = k;
+    if (wg == 0)
+        G.dn[item] = d;
+}
+
+// Gate/up of the device-resident block at decode shapes, planning its own item from the
+// segments (no planner launch): wave 0 builds the descriptor in LDS, then the workgroup
+// runs the task as the compact-descriptor kernel does.
+template <int FMT, int TERMS, int KS, int SR, bool PACK>
+__global__ __launch_bounds__(kDecThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void k_mfma_dec_seg(DecArgs A, DecSegArgs G) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    const int item = blockIdx.x / A.wgs, wg = blockIdx.x - item * A.wgs;
+    DecDescK *kd = reinterpret_cast<DecDescK *>(smem + G.kd_off);
+    if (threadIdx.x < 64)
+        seg_plan(G, item, wg, (int)threadIdx.x, kd);
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane((int)kd->nrow) == 0)
+        return;  // past the call's items (the whole workgroup)
+    dec_task<FMT, true, TERMS, KS, 2, SR, PACK, true>(A, 0, wg, (int)threadIdx.x, smem, kd);
+}
+
 size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks, int nt) {
     (void)dual;
     return dec_lds_plan(fmt, K, rmax, terms, ks, nt, nullptr);
@@ -62,8 +165,12 @@ static hipError_t lds_limit(const void *f, size_t lds) {
 }
 
 template <int FMT, bool DUAL, int TERMS, int KS, int NT>
-static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const DecDescK *inl) {
+static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const DecDescK *inl,
+                               const DecSegArgs *seg) {
     const size_t lds = mfma_dec_lds_bytes(FMT, a.K, a.rmax, TERMS, DUAL, KS, NT);
+    // the self-planning kernel keeps its descriptor past the task's LDS
+    const size_t kd_off = (lds + 15) & ~(size_t)15;
+    const size_t lds_seg = kd_off + sizeof(DecDescK);
     const int tiles_wg = (kDecWaves / KS) * (DUAL ? 1 : NT);  // column tiles per workgroup
     if (a.K % 512 || a.K % (256 * KS) || a.K / KS > dec_max_kr(FMT) || a.O % (16 * tiles_wg) ||
         a.rmax < 1 || a.rmax > 16 ||
@@ -79,11 +186,26 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const Dec
     const int sr = (int)((need + kDecThreads - 1) / kDecThreads);
     if (inl && (!DUAL || n_items > kDecInline))
         return hipErrorInvalidValue;
+    if (seg && (!DUAL || inl || a.n_cp || a.n_items_dev || lds_seg > kDecLdsBudget))
+        return hipErrorInvalidValue;
+    DecSegArgs sg{};
+    if (seg) {
+        sg = *seg;
+        sg.kd_off = (int)kd_off;
+    }
     DecInline di;
     if (inl)
         std::copy(inl, inl + n_items, di.d);
-    auto go = [&](auto kern, auto kern_inl, auto has_inl) {
+    auto go = [&](auto kern, auto kern_inl, auto kern_seg, auto has_inl) {
         constexpr bool HI = decltype(has_inl)::value;
+        if constexpr (HI) {
+            if (seg) {
+                hipError_t e = lds_limit(reinterpret_cast<const void *>(kern_seg), lds_seg);
+                if (e == hipSuccess)
+                    hipLaunchKernelGGL(kern_seg, grid, block, lds_seg, st, a, sg);
+                return e;
+            }
+        }
         const void *f = HI && inl ? reinterpret_cast<const void *>(kern_inl)
                                   : reinterpret_cast<const void *>(kern);
         hipError_t e = lds_limit(f, lds);
@@ -103,9 +225,10 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const Dec
         constexpr int SRv = decltype(sr_c)::value;
         constexpr bool PKv = decltype(pack_c)::value;
         if constexpr (DUAL && NT == 2)
-            return go(kern, k_mfma_dec_inl<FMT, TERMS, KS, SRv, PKv>, std::true_type{});
+            return go(kern, k_mfma_dec_inl<FMT, TERMS, KS, SRv, PKv>,
+                      k_mfma_dec_seg<FMT, TERMS, KS, SRv, PKv>, std::true_type{});
         else
-            return go(kern, kern, std::false_type{});
+            return go(kern, kern, kern, std::false_type{});
     };
     hipError_t e;
     constexpr int SR1 = DUAL ? 2 : 4, SR2 = DUAL ? kDecStageDual : kDecStageSingle;
@@ -137,26 +260,26 @@ static hipError_t launch_dec_t(DecArgs a, int n_items, hipStream_t st, const Dec
 
 template <int FMT, bool DUAL, int TERMS>
 static hipError_t launch_dec_k(const DecArgs &a, int n_items, int ks, int nt, hipStream_t st,
-                               const DecDescK *inl) {
+                               const DecDescK *inl, const DecSegArgs *seg) {
     if constexpr (DUAL) {
         if (nt != 2)
             return hipErrorInvalidValue;
         switch (ks) {
-        case 1: return launch_dec_t<FMT, true, TERMS, 1, 2>(a, n_items, st, inl);
-        case 2: return launch_dec_t<FMT, true, TERMS, 2, 2>(a, n_items, st, inl);
-        case 4: return launch_dec_t<FMT, true, TERMS, 4, 2>(a, n_items, st, inl);
-        case 8: return launch_dec_t<FMT, true, TERMS, 8, 2>(a, n_items, st, inl);
+        case 1: return launch_dec_t<FMT, true, TERMS, 1, 2>(a, n_items, st, inl, seg);
+        case 2: return launch_dec_t<FMT, true, TERMS, 2, 2>(a, n_items, st, inl, seg);
+        case 4: return launch_dec_t<FMT, true, TERMS, 4, 2>(a, n_items, st, inl, seg);
+        case 8: return launch_dec_t<FMT, true, TERMS, 8, 2>(a, n_items, st, inl, seg);
         default: return hipErrorInvalidValue;
         }
     } else {
         if (nt == 2)
-            return ks == 1 ? launch_dec_t<FMT, false, TERMS, 1, 2>(a, n_items, st, inl)
+            return ks == 1 ? launch_dec_t<FMT, false, TERMS, 1, 2>(a, n_items, st, inl, seg)
                            : hipErrorInvalidValue;
         switch (ks) {
-        case 1: return launch_dec_t<FMT, false, TERMS, 1, 1>(a, n_items, st, inl);
-        case 2: return launch_dec_t<FMT, false, TERMS, 2, 1>(a, n_items, st, inl);
-        case 4: return launch_dec_t<FMT, false, TERMS, 4, 1>(a, n_items, st, inl);
-        case 8: return launch_dec_t<FMT, false, TERMS, 8, 1>(a, n_items, st, inl);
+        case 1: return launch_dec_t<FMT, false, TERMS, 1, 1>(a, n_items, st, inl, seg);
+        case 2: return launch_dec_t<FMT, false, TERMS, 2, 1>(a, n_items, st, inl, seg);
+        case 4: return launch_dec_t<FMT, false, TERMS, 4, 1>(a, n_items, st, inl, seg);
+        case 8: return launch_dec_t<FMT, false, TERMS, 8, 1>(a, n_items, st, inl, seg);
         default: return hipErrorInvalidValue;
         }
     }
@@ -164,12 +287,13 @@ static hipError_t launch_dec_k(const DecArgs &a, int n_items, int ks, int nt, hi
 
 template <int FMT, bool DUAL>
 static hipError_t launch_dec_fd(const DecArgs &a, int n_items, int terms, int ks, int nt,
-                                hipStream_t st, const DecDescK *inl) {
+                                hipStream_t st, const DecDescK *inl,
+                                const DecSegArgs *seg) {
     if (terms <= 1)
-        return launch_dec_k<FMT, DUAL, 1>(a, n_items, ks, nt, st, inl);
+        return launch_dec_k<FMT, DUAL, 1>(a, n_items, ks, nt, st, inl, seg);
     if (terms == 2)
-        return launch_dec_k<FMT, DUAL, 2>(a, n_items, ks, nt, st, inl);
-    return launch_dec_k<FMT, DUAL, 3>(a, n_items, ks, nt, st, inl);
+        return launch_dec_k<FMT, DUAL, 2>(a, n_items, ks, nt, st, inl, seg);
+    return launch_dec_k<FMT, DUAL, 3>(a, n_items, ks, nt, st, inl, seg);
 }
 
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
@@ -177,10 +301,14 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
                            const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
-                           const DecDescK *inl, const int *n_items_dev) {
+                           const DecDescK *inl, const int *n_items_dev, const DecSegArgs *seg) {
     if (n_items <= 0)
         return n_cp > 0 ? hipErrorInvalidValue : hipSuccess;
     if (K > kDecMaxK || (n_items_dev && (inl || n_cp > 0)))
+        return hipErrorInvalidValue;
+    if (seg && (seg->rmax != rmax || seg->cap_items != n_items || seg->cap_rows > 65535 ||
+                seg->cap_rows > rcap || seg->S > 65535 || seg->cap_e < 0 || !seg->dn ||
+                !seg->n_items || !seg->err))
         return hipErrorInvalidValue;
     DecArgs a{};
     a.n_items_dev = n_items_dev;
@@ -204,11 +332,11 @@ hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const 
     a.n_cp = n_cp;
     a.pack = pack ? 1 : 0;
     if (fmt == 4)
-        return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st, inl)
-                    : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st, inl);
+        return dual ? launch_dec_fd<4, true>(a, n_items, terms, ks, nt, st, inl, seg)
+                    : launch_dec_fd<4, false>(a, n_items, terms, ks, nt, st, inl, seg);
     if (fmt == 7)
-        return dual ? launch_dec_fd<7, true>(a, n_items, terms, ks, nt, st, inl)
-                    : launch_dec_fd<7, false>(a, n_items, terms, ks, nt, st, inl);
+        return dual ? launch_dec_fd<7, true>(a, n_items, terms, ks, nt, st, inl, seg)
+                    : launch_dec_fd<7, false>(a, n_items, terms, ks, nt, st, inl, seg);
     return hipErrorInvalidValue;
 }
 

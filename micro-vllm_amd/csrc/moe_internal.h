@@ -119,6 +119,25 @@ struct DecInline {
     DecDescK d[kDecInline];
 };
 
+// Segments of a call on device-resident segments for the gate/up decode kernel that plans
+// its own item (k_mfma_dec_seg, the device-resident block at decode shapes): wave 0 of each
+// workgroup finds item blockIdx / wgs among the live segments (items of rmax rows in
+// segment order, as k_dplan_dec numbers them) and builds its descriptor in LDS at byte
+// kd_off; column block 0 of each item writes the item's down descriptor to dn, and
+// workgroup 0 the item count and the status.
+struct DecSegArgs {
+    const void *const *table;  // blob address per expert id (device)
+    int n_table;
+    long long off[6];          // piece offsets: gate_p gate_s up_p up_s down_p down_s
+    const int *counts, *eids, *xoff, *nr, *rows;
+    const float *rw;
+    int cap_e, cap_rows, S, rmax, cap_items;
+    int kd_off;                // LDS byte offset of the descriptor (past the task's LDS)
+    DecDesc *dn;               // [cap_items]
+    int *n_items;              // [1]
+    int *err;                  // 0, or 2: a blob address not 256-byte aligned (skipped)
+};
+
 // The gate/up kernel (dual) reads the f32 input rows and splits them into `terms` bf16
 // terms in LDS; each wave computes the gate and the up tile of the same 16 columns over
 // K / ks and applies the activation in registers (ks > 1: partial sums meet in LDS).  It
@@ -145,13 +164,16 @@ size_t mfma_dec_lds_bytes(int fmt, int K, int rmax, int terms, int dual, int ks,
 // inl (dual only, optional): the n_items (<= kDecInline) descriptors in the compact form,
 // in host memory; copied into the kernel arguments, and desc is not read.
 // n_items_dev (optional, not with inl or n_cp): the item count in device memory; n_items
-// is then the capacity the grid covers.
+// is then the capacity the grid covers.  seg (dual only, not with inl, n_cp or
+// n_items_dev): the gate/up kernel plans its items from the segments (DecSegArgs); desc
+// is not read and n_items is the capacity.
 hipError_t launch_mfma_dec(int fmt, bool dual, int terms, int ks, int nt, const DecDesc *desc,
                            int n_items, const float *xin, const void *pin, const float *xs,
                            void *pout, float *hp, float *out, int K, int O, int rcap, int rmax,
                            int act, float act_a, float act_b, bool fold, bool pack,
                            const DecDesc *cp_src, DecDesc *cp_dst, int n_cp, hipStream_t st,
-                           const DecDescK *inl = nullptr, const int *n_items_dev = nullptr);
+                           const DecDescK *inl = nullptr, const int *n_items_dev = nullptr,
+                           const DecSegArgs *seg = nullptr);
 
 // Grouped GEMM (kern_gemm.hip), the prefill path: items {expert, r0, nrow, 0} with
 // nrow <= 16 * mt (mt in 1, 2, 4, 8, up to gemm_max_mt); one workgroup of 8 waves per

@@ -1808,11 +1808,12 @@ int promote_locked(Ctx &C, const void *host_blob, size_t bytes, int layer, int e
     return 1;
 }
 
-// mvllm_hip_moe_block_routed_dev at decode shapes (S <= 16 out rows): the decode kernels
-// on descriptors the device planner writes (k_dplan_dec), the top-k combine folded into
-// the down kernel as in the host-planned decode call, or with option combine_ordered the
-// ordered combine on device-built lists.  Three launches (five ordered) where the
-// grouped-GEMM path takes fifteen.  Returns -1 when the shapes do not take this path (the
+// mvllm_hip_moe_block_routed_dev at decode shapes (S <= 16 out rows): the decode kernels,
+// the top-k combine folded into the down kernel as in the host-planned decode call, the
+// gate/up kernel planning its own item from the segments and writing the down
+// descriptors (k_mfma_dec_seg); or, with option combine_ordered, on descriptors the
+// device planner writes (k_dplan_dec) with the ordered combine on device-built lists.
+// Two launches (six ordered) where the grouped-GEMM path takes fifteen.  Returns -1 when the shapes do not take this path (the
 // caller runs the grouped GEMM), else the entry's result.  Arguments validated by the
 // caller, which holds C.mu.
 int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_table,
@@ -1879,11 +1880,43 @@ int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_ta
     a.n_items = reinterpret_cast<int *>(misc);
     a.err = status ? status : reinterpret_cast<int *>(misc + 64);
     a.row_ok = reinterpret_cast<unsigned char *>(misc + b_misc);
-    HIP_TRY(launch_dplan_dec(a, st));
     float *hp = fmt == 4 ? static_cast<float *>(C.HP.p) : nullptr;
-    HIP_TRY(launch_mfma_dec(fmt, true, terms, gu.ks, gu.nt, a.gu, cap_items, x, nullptr, nullptr,
-                            C.Ph.p, hp, nullptr, D, I, cap_rows, rmax, act, act_a, act_b, false,
-                            pk, nullptr, nullptr, 0, st, nullptr, a.n_items));
+    // with the combine folded into the down kernel, the gate/up kernel plans its own items
+    // (the compact descriptor: 16-bit compact rows, 32-bit piece offsets); the ordered
+    // combine needs the planner's row flags
+    bool self_plan = fold && cap_rows <= 65535;
+    for (int k = 1; k < 4; ++k)
+        self_plan = self_plan && std::llabs(off6[k] - off6[0]) < (1ll << 31);
+    if (self_plan) {
+        DecSegArgs sg{};
+        sg.table = table;
+        sg.n_table = n_table;
+        for (int k = 0; k < 6; ++k)
+            sg.off[k] = off6[k];
+        sg.counts = counts;
+        sg.eids = eids;
+        sg.xoff = xoff;
+        sg.nr = nr;
+        sg.rows = rows;
+        sg.rw = rw;
+        sg.cap_e = cap_experts;
+        sg.cap_rows = cap_rows;
+        sg.S = S;
+        sg.rmax = rmax;
+        sg.cap_items = cap_items;
+        sg.dn = a.dn;
+        sg.n_items = a.n_items;
+        sg.err = a.err;
+        HIP_TRY(launch_mfma_dec(fmt, true, terms, gu.ks, gu.nt, nullptr, cap_items, x, nullptr,
+                                nullptr, C.Ph.p, hp, nullptr, D, I, cap_rows, rmax, act, act_a,
+                                act_b, false, pk, nullptr, nullptr, 0, st, nullptr, nullptr,
+                                &sg));
+    } else {
+        HIP_TRY(launch_dplan_dec(a, st));
+        HIP_TRY(launch_mfma_dec(fmt, true, terms, gu.ks, gu.nt, a.gu, cap_items, x, nullptr,
+                                nullptr, C.Ph.p, hp, nullptr, D, I, cap_rows, rmax, act, act_a,
+                                act_b, false, pk, nullptr, nullptr, 0, st, nullptr, a.n_items));
+    }
     HIP_TRY(launch_mfma_dec(fmt, false, terms, dn.ks, dn.nt, a.dn, cap_items, nullptr, C.Ph.p, hp,
                             nullptr, nullptr, fold ? out : static_cast<float *>(C.Y.p), I, D,
                             cap_rows, rmax, 0, 0.f, 0.f, fold, pk, nullptr, nullptr, 0, st,
