@@ -127,10 +127,6 @@ int mvllm_hip_moe_block_dev_noalloc(int nb, int D, int Iinter, int fmt, int qgs,
  *            GEMM run a kernel with wide wave tiles (8 waves of 128 rows x 64 weight
  *            columns), 0 = the grouped GEMM's own 128-row class.  Same products; sums in
  *            another order.
- *   "gemm_down_blocks" 1, 2 (default) or 4 = column blocks of 256 per down-projection
- *            task of the one-term grouped GEMM, run one after the other with the next
- *            block's first K steps loaded during the last steps of the one before (fewer
- *            where they do not divide D or K / 256 is odd).  Same results.
  *   "combine_ordered" 1 = decode calls of mvllm_hip_moe_block_dev also run the separate
  *            combine kernel, which applies out[t] += w * y in the reference's expert order
  *            (bit-exact given the same expert outputs); by default they fold the combine

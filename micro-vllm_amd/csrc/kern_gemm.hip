@@ -45,9 +45,6 @@ struct GemmArgs {
     float *out;         // single: Y [rcap][O] f32; dual: H [rcap][O] f32 instead of planes
                         // when set (the native-MXFP4 call quantizes H afterwards)
     int nbn;            // column blocks per item
-    int nh;             // down form: 256-column blocks per task, run one after the other
-                        // with the loads of the next block's first steps issued during
-                        // the last steps of the one before (1: one block)
     int n_tasks;        // items * nbn
     const int *n_items_dev;  // non-null: the item count is in device memory (a grid sized
                              // for its bound; workgroups past items * nbn exit)
@@ -114,13 +111,10 @@ struct TaskD {
 // grouped form no registers).  The 32-row class with one term is held to 128 VGPRs (4 waves
 // per SIMD), so two workgroups share a CU: the grouped form needs 110-120 (its A tiles go
 // straight into LDS), the dense-linear form 126-131, where the cap costs at most a few
-// spilled registers (c3 with register-staged A tiles: 1.60 -> 1.53 ms per call).  The
-// one-term 16-row down form is held to the same cap: its block loop (multi-block tasks)
-// needs 124-137, and what the cap spills is reloaded between blocks, not in the K loop.
+// spilled registers (c3 with register-staged A tiles: 1.60 -> 1.53 ms per call).
 template <int FMT, bool DUAL, int TERMS, int MT, bool UNI>
 __global__ __launch_bounds__(kGemmThreads)
-__attribute__((amdgpu_waves_per_eu(TERMS == 1 && (MT == 2 || (MT == 1 && !DUAL)) ? 4 : 1, 8)))
-void k_gemm(GemmArgs A) {
+__attribute__((amdgpu_waves_per_eu(MT == 2 && TERMS == 1 ? 4 : 1, 8))) void k_gemm(GemmArgs A) {
     // scales in 64-byte chunks (GScaleC) where the registers allow (not the MXFP4 down
     // kernel of the 32-row class: it would pass its 128-VGPR cap and spill)
     constexpr bool kChunkS = !UNI && TERMS == 1 && MT <= 4 && !(FMT == 7 && !DUAL && MT == 2);
@@ -155,23 +149,6 @@ void k_gemm(GemmArgs A) {
     const uint32_t rowb = (uint32_t)(K >> 1);
     const uint32_t srow = (uint32_t)(FMT == 4 ? (K / 64) * 4 : K / 32);
     const int nk = K / kGemmBK;
-    // multi-block tasks: the one-term down form
-    constexpr bool kMulti = !DUAL && !UNI && TERMS == 1;
-    const int nh = kMulti ? A.nh : 1;
-    // (half, step) of the step d ahead of step k of block h: into the next block, or the
-    // task's last step again past its end
-    auto ahead = [&] __attribute__((always_inline)) (int h, int k, int d, int &ht, int &kt) {
-        kt = k + d;
-        ht = h;
-        if (kt >= nk) {
-            if (h + 1 < nh) {
-                ht = h + 1;
-                kt -= nk;
-            } else {
-                kt = nk - 1;
-            }
-        }
-    };
 
     auto make_task = [&] __attribute__((always_inline)) (int task) {
         TaskD<FMT> d;
@@ -200,7 +177,7 @@ void k_gemm(GemmArgs A) {
         const ExpertWork &ew = UNI ? A.ew1 : A.ew[it.a];
         d.jbase = ew.row0 + it.r0;
         d.nrow = it.nrow;
-        d.col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 * nh + wave * 32;
+        d.col0 = DUAL ? nb * 128 + wave * 16 : nb * 256 + wave * 32;
 #pragma unroll
         for (int m = 0; m < 2; ++m) {
             const int mi = DUAL ? m : 2;
@@ -214,32 +191,29 @@ void k_gemm(GemmArgs A) {
         return d;
     };
 
-    // weights of step k of column block h (down form: 256 weight rows further per block)
-    auto load_b = [&] __attribute__((always_inline)) (GStep<FMT> &b, const TaskD<FMT> &d, int h,
-                                                       int k) {
-        const uint32_t so = (uint32_t)k * 128u + (uint32_t)h * 256u * rowb;
+    auto load_b = [&] __attribute__((always_inline)) (GStep<FMT> &b, const TaskD<FMT> &d, int k) {
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 b.w[m][g] = __builtin_bit_cast(
-                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rw[m], d.vw[m] + 32 * g, so, 0));
+                    u32x2, __builtin_amdgcn_raw_buffer_load_b64(d.rw[m], d.vw[m] + 32 * g,
+                                                                (uint32_t)k * 128u, 0));
     };
     // scales of the pair holding step k; chunked: the chunk holding step k, loaded only
     // when step k opens the chunk (otherwise the offset lies past the buffer, which loads
     // zeros without touching memory and keeps the body free of branches)
-    auto load_s = [&] __attribute__((always_inline)) (Scl &s, const TaskD<FMT> &d, int h, int k) {
-        const uint32_t ho = (uint32_t)h * 256u * srow;
+    auto load_s = [&] __attribute__((always_inline)) (Scl &s, const TaskD<FMT> &d, int k) {
         if constexpr (kChunkS) {
             const bool open = ((k >> 1) % PPC) == 0;
-            const uint32_t off = (uint32_t)((k >> 1) / PPC) * 64u + ho;
+            const uint32_t off = (uint32_t)((k >> 1) / PPC) * 64u;
 #pragma unroll
             for (int m = 0; m < 2; ++m)
                 s.c[m] = __builtin_bit_cast(
                     u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                d.rs[m], open ? d.vs[m] + off : 0xffffff00u, 0, 0));
         } else {
-            const uint32_t off = (uint32_t)(k >> 1) * (FMT == 4 ? 32u : 16u) + ho;
+            const uint32_t off = (uint32_t)(k >> 1) * (FMT == 4 ? 32u : 16u);
 #pragma unroll
             for (int m = 0; m < 2; ++m) {
                 if constexpr (FMT == 4)
@@ -611,23 +585,19 @@ void k_gemm(GemmArgs A) {
         }
     };
 
-    // epilogue of column block h of one task: C[4 q + i][t] of row tile mt and tile m
-    auto epilogue = [&] __attribute__((always_inline)) (const TaskD<FMT> &d, int h) {
-        int c0 = d.col0 + 256 * h, jb = d.jbase;
-        // opaque here: inside the block loop of multi-block tasks, the compiler would
-        // otherwise keep every row's output address live through the loop
-        asm volatile("" : "+s"(c0), "+s"(jb));
+    // epilogue of one task: C[4 q + i][t] of row tile mt and tile m
+    auto epilogue = [&] __attribute__((always_inline)) (const TaskD<FMT> &d) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = mt * 16 + 4 * q + i;
-                const int j = jb + r;
+                const int j = d.jbase + r;
                 if constexpr (DUAL) {
                     const float h = mf_act(A.act, acc[mt][0][i], acc[mt][1][i], A.act_a, A.act_b);
                     __bf16 tt[3];
                     split_terms<TERMS>(h, tt);
-                    const int col = c0 + t;
+                    const int col = d.col0 + t;
                     const int pos = (col & ~7) + a_slot<FMT>(col & 7);
                     if (r < d.nrow) {
                         if (A.out) {
@@ -640,8 +610,8 @@ void k_gemm(GemmArgs A) {
                     }
                 } else {
                     if (r < d.nrow) {
-                        A.out[(size_t)j * O + c0 + t] = acc[mt][0][i];
-                        A.out[(size_t)j * O + c0 + 16 + t] = acc[mt][1][i];
+                        A.out[(size_t)j * O + d.col0 + t] = acc[mt][0][i];
+                        A.out[(size_t)j * O + d.col0 + 16 + t] = acc[mt][1][i];
                     }
                 }
             }
@@ -670,12 +640,12 @@ void k_gemm(GemmArgs A) {
             dma_a(cur, 0, 0);
         else
             load_a(ra0, cur, 0);
-        load_b(b0, cur, 0, 0);
-        load_s(sn, cur, 0, 0);
+        load_b(b0, cur, 0);
+        load_s(sn, cur, 0);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (PA == 2)
             load_a(ra1, cur, min(1, nk - 1));
-        load_b(b1, cur, 0, min(1, nk - 1));
+        load_b(b1, cur, min(1, nk - 1));
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (!kDmaA)
             store_a(ra0, 0);
@@ -685,12 +655,8 @@ void k_gemm(GemmArgs A) {
     // past the task's last step read its last step again (L2 hits, never consumed):
     // wrapping to the first steps instead re-read two steps of weights from HBM per task,
     // a quarter of the bytes at K = 2048.
-    // Blocks of a multi-block task (nh > 1, nk even) continue the pipeline: the last
-    // steps of block h prefetch the first steps of block h + 1 (same A rows, weights 256
-    // rows on).
-    auto step_even = [&] __attribute__((always_inline)) (int h, int k, auto exact) {
-        int h2, k2;
-        ahead(h, k, 2, h2, k2);
+    auto step_even = [&] __attribute__((always_inline)) (int k, auto exact) {
+        const int k2 = min(k + 2, nk - 1);
         if constexpr (kChunkS) {
             // a new chunk opens at this pair: the chunk loaded two steps ago
             if (((k >> 1) % PPC) == 0)
@@ -706,26 +672,24 @@ void k_gemm(GemmArgs A) {
             load_a(ra1, cur, min(k + 1, nk - 1));
         compute(b0, 0, sc, k >> 1, 0, exact);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b0, cur, h2, k2);
-        load_s(sn, cur, h2, k2);
+        load_b(b0, cur, k2);
+        load_s(sn, cur, k2);
         if constexpr (!kDmaA)
             store_a(ra1, 1);
         __syncthreads();
     };
     // odd step k + 1: LDS buffer 1, weights b1; stages A(k + 2) into buffer 0
-    auto step_odd = [&] __attribute__((always_inline)) (int h, int k, auto exact) {
-        int h3, k3, h2, k2;
-        ahead(h, k, 3, h3, k3);
-        ahead(h, k, 2, h2, k2);  // the A rows are the same in every block: step k2
+    auto step_odd = [&] __attribute__((always_inline)) (int k, auto exact) {
+        const int k3 = min(k + 3, nk - 1);
         if constexpr (kDmaA)
-            dma_a(cur, k2, 0);
+            dma_a(cur, min(k + 2, nk - 1), 0);
         else if constexpr (PA == 2)
             load_a(ra1, cur, k3);
         else
-            load_a(ra0, cur, k2);
+            load_a(ra0, cur, min(k + 2, nk - 1));
         compute(b1, 1, sc, k >> 1, 1, exact);
         __builtin_amdgcn_sched_barrier(0);
-        load_b(b1, cur, h3, k3);
+        load_b(b1, cur, k3);
         if constexpr (!kDmaA)
             store_a(ra0, 0);
         __syncthreads();
@@ -734,37 +698,29 @@ void k_gemm(GemmArgs A) {
     // compiler with the loop test, gives a path from the even step straight back to the
     // loop head, on which the wait counts would also wait for step k + 1's weights.  An
     // odd last step runs after the loop.
-    // Multi-block tasks write each column block's results as its last step ends.
     auto k_loop = [&] __attribute__((always_inline)) (auto exact) {
-        for (int h = 0; h < nh; ++h) {
-            for (int k = 0; k + 2 <= nk; k += 2) {
-                step_even(h, k, exact);
-                step_odd(h, k, exact);
-            }
-            if (nk & 1)
-                step_even(h, nk - 1, exact);
-            if constexpr (kMulti)
-                epilogue(cur, h);
+        for (int k = 0; k + 2 <= nk; k += 2) {
+            step_even(k, exact);
+            step_odd(k, exact);
         }
+        if (nk & 1)
+            step_even(nk - 1, exact);
     };
     prologue();
     k_loop(std::false_type{});
     // Rare second pass: some operand of the task needs the exact decode.  The whole
-    // workgroup runs the task again (the A staging is shared) and writes its results over
-    // the first pass's.  (The same loop with a uniform branch per step instead of this
-    // second copy raised the register count of the common pass.)
+    // workgroup runs the task again (the A staging is shared).  (The same loop with a
+    // uniform branch per step instead of this second copy raised the register count of
+    // the common pass.)
     if (__syncthreads_or((int)exc)) {
         exc = 0;
-        if constexpr (!kMulti) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
-        }
+        for (int mt = 0; mt < MT; ++mt)
+            acc[mt][0] = acc[mt][1] = f4v{0.f, 0.f, 0.f, 0.f};
         prologue();
         k_loop(std::true_type{});
     }
-    if constexpr (!kMulti)
-        epilogue(cur, 0);
+    epilogue(cur);
 }
 
 // ---- input planes for the GEMM: gather, split into bf16 terms ------------------------
@@ -829,9 +785,6 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep_planes(const float *x,
 static bool g_gemm_xcd = true;  // option "gemm_xcd"
 void gemm_set_xcd(bool on) { g_gemm_xcd = on; }
 bool gemm_xcd() { return g_gemm_xcd; }
-static int g_gemm_nh = 2;  // option "gemm_down_blocks"
-void gemm_set_down_blocks(int v) { g_gemm_nh = v; }
-int gemm_down_blocks() { return g_gemm_nh; }
 
 template <int FMT, bool DUAL, int TERMS, int MT, bool UNI = false>
 static hipError_t launch_gemm_t(GemmArgs a, int n_items, hipStream_t st) {
@@ -893,13 +846,7 @@ hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *
     a.pin = static_cast<const __bf16 *>(pin);
     a.pout = static_cast<__bf16 *>(pout);
     a.out = out;
-    // down form: nh column blocks of 256 per task where they divide O and the pipeline's
-    // step pairs do not straddle two blocks (K / 256 even)
-    int nh = dual || terms != 1 ? 1 : std::max(1, g_gemm_nh);
-    while (nh > 1 && (O % (256 * nh) || (K / kGemmBK) % 2))
-        nh >>= 1;
-    a.nh = nh;
-    a.nbn = O / (dual ? 128 : 256 * nh);
+    a.nbn = O / (dual ? 128 : 256);
     a.K = K;
     a.O = O;
     a.rcap = rcap;
@@ -928,7 +875,6 @@ hipError_t launch_gemm_rows(int fmt, int terms, int mt, const ExpertWork *ew1, i
     a.pin = static_cast<const __bf16 *>(pin);
     a.out = out;
     a.nbn = O / 256;
-    a.nh = 1;
     a.K = K;
     a.O = O;
     a.rcap = nrows;

@@ -191,13 +191,6 @@ size_t gemm_lds_bytes(int fmt, int terms, int mt);
 // range of tasks (an item's column blocks share one L2), 0 = task = workgroup index.
 void gemm_set_xcd(bool on);
 bool gemm_xcd();
-// Column blocks of 256 per down-projection task of the grouped GEMM (option
-// "gemm_down_blocks", default 2; 1, 2 or 4): a task runs its blocks one after the other,
-// the first steps of each block loaded during the last steps of the one before, so the
-// short K loop of the down projection (K = Iinter) restarts its pipeline less often.
-// Fewer where they do not divide D or K / 256 is odd.
-void gemm_set_down_blocks(int v);
-int gemm_down_blocks();
 // dual with out set: H is written to out as f32 rows [rcap][O] instead of planes to pout.
 hipError_t launch_gemm(int fmt, bool dual, int terms, int mt, const ExpertWork *ew,
                        const void *items, int n_items, const void *pin, void *pout, float *out,

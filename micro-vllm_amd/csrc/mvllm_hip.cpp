@@ -1450,10 +1450,6 @@ int mvllm_hip_set_option(const char *key, long long value) {
         C.dec_ks = static_cast<int>(value);
     } else if (k == "gemm_xcd") {
         gemm_set_xcd(value != 0);
-    } else if (k == "gemm_down_blocks") {
-        if (value != 1 && value != 2 && value != 4)
-            return 0;
-        gemm_set_down_blocks(static_cast<int>(value));
     } else if (k == "gemm_wide") {
         if (value < 0 || value > 1)
             return 0;

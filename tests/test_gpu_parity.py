@@ -583,31 +583,6 @@ def test_gemm_task_order(hip, case):
     assert np.array_equal(base.view(np.uint32), other.view(np.uint32))
 
 
-@pytest.mark.parametrize("case", [GEMM_CASES[0], GEMM_CASES[3], GEMM_CASES[4],
-                                  (7, 7168, 2048, [130, 3, 17, 40], 64, 2, 4.0, 25.0, (), 1),
-                                  (4, 6144, 2048, [16, 27, 5], 48, 1, 7.0, 0.0, (1,), 2)])
-def test_gemm_down_blocks(hip, case):
-    """Option gemm_down_blocks (1, 2, 4 column blocks of 256 per down task, the pipeline
-    running on from block to block) changes which workgroup computes a column block, not
-    its tiles or summation: results are bit-identical.  GEMM_CASES[4] (K = 768, three
-    steps) falls back to one block a task."""
-    fmt, D, I, nr, S, act, a, b, nulls, bad = case
-    say("gemm down blocks", case)
-    rng = np.random.default_rng(D * 13 + I + sum(nr))
-    c = random_case(rng, fmt, D, I, nr, S, act, a, b, nulls, bad)
-    outs = {}
-    try:
-        for nh in (1, 2, 4):
-            assert hip.set_option("gemm_down_blocks", nh)
-            outs[nh] = _gemm_run(hip, c, 0)
-    finally:
-        hip.set_option("gemm_down_blocks", 2)
-    assert not hip.set_option("gemm_down_blocks", 3)
-    for nh in (2, 4):
-        assert np.array_equal(outs[1].view(np.uint32), outs[nh].view(np.uint32)), nh
-    assert npref.rel_err(outs[2], npref.moe_block64(*c.args(), act, a, b)) < TOL_BF16
-
-
 @pytest.mark.parametrize("fmt,D,I,nr,act,a,b", [
     (4, 6144, 2048, [40, 21, 1], 1, 7.0, 0.0),          # c3 shapes
     (7, 7168, 2048, [130, 3, 17], 2, 4.0, 25.0),         # c4 shapes, a full 128-row block

@@ -6,11 +6,7 @@ change that adds live registers makes the compiler spill to scratch memory, whic
 ~15 % per call when it happened.  The bars are the spill bytes of the kept build: none
 for the 16- and 64-row classes, the FP4, f32 and wide-tile GEMMs (the eight-wave form, the
 default; each of its waves must stay within 256 VGPRs, two waves per SIMD); at most 32
-bytes elsewhere, except the one-term down forms of the 16- and 32-row classes (held to 128
-VGPRs with their column-block loop): at most 64 bytes.  What costs time is a spill inside
-the K loop, so the innermost loops are checked too: no scratch access in them, except one
-8-byte reload per step pair in the one-term 16-row MXFP4 down form (and two in its rare
-exact pass).
+bytes elsewhere.
 """
 import os
 import re
@@ -29,35 +25,12 @@ def kernel_resources(src, tmp_path):
                     "-target-feature", "-Xclang", "-packed-fp32-ops", "--cuda-device-only",
                     "-S", "-o", str(out), src], check=True, capture_output=True)
     text = out.read_text()
-    kernel_resources.loops = loop_scratch(text)
     res = {}
     for m in re.finditer(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", text, re.S):
         body = m.group(2)
         res[m.group(1)] = (int(re.search(r"private_segment_fixed_size (\d+)", body).group(1)),
                            int(re.search(r"next_free_vgpr (\d+)", body).group(1)))
     return res
-
-
-def loop_scratch(asm_text):
-    """Scratch instructions inside each kernel's innermost loops: from a label the compiler
-    marks as an inner loop header to the branch back to it."""
-    out = {}
-    for m in re.finditer(r"^(_Z\S+):[^\n]*\n(.*?)s_endpgm", asm_text, re.S | re.M):
-        lines = m.group(2).split("\n")
-        cnt = 0
-        for i, line in enumerate(lines):
-            # the mark is on the label's line, or on the next one (nested loops)
-            h = re.match(r"^(\.LBB\d+_\d+):", line)
-            nxt = lines[i + 1] if i + 1 < len(lines) else ""
-            if not h or ("Inner Loop Header" not in line and "Inner Loop Header" not in nxt):
-                continue
-            back = re.compile(r"s_c?branch\S*\s+" + re.escape(h.group(1)) + r"\b")
-            for j in range(i + 1, len(lines)):
-                if back.search(lines[j]):
-                    cnt += sum(1 for x in lines[i:j] if "scratch_" in x)
-                    break
-        out[m.group(1)] = cnt
-    return out
 
 
 def demangle(names):
@@ -76,15 +49,10 @@ def test_gemm_classes_within_register_budget(tmp_path):
         if not m:
             continue
         seen += 1
-        fmt, dual, terms, mt = int(m.group(1)), m.group(2) == "true", int(m.group(3)), int(m.group(4))
-        uni = m.group(5) == "true"
-        multi = not dual and not uni and terms == 1 and mt <= 2
-        bar = 64 if multi else 0 if mt in (1, 4) else 32
+        mt = int(m.group(4))
+        bar = 0 if mt in (1, 4) else 32
         assert scratch <= bar, f"{names[mangled]}: {scratch} bytes of scratch (bar {bar})"
         assert vgpr <= 256
-        in_loops = kernel_resources.loops.get(mangled, 0)
-        loop_bar = 3 if multi and fmt == 7 and mt == 1 else 0
-        assert in_loops <= loop_bar, f"{names[mangled]}: {in_loops} scratch accesses in K loops"
     assert seen >= 28
 
 
