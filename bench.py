@@ -361,7 +361,8 @@ def routed_prefill(np, torch, mvllm_hip, w, pool, cfg, T, steps, warmup):
     workload's segments in device memory (as mvllm_hip_moe_route_dev leaves them) with a
     device table of the pool layer's blobs, against the host-planned moe_block_dev call on
     the same segments and the same rotation of pool layers (HIP events around `steps`
-    calls of each, after `warmup`).  Both write the same out rows; the routed call plans on
+    calls of each, after `warmup`), in the default bf16 arithmetic and with native MXFP4
+    activations (option fp4act).  Both write the same out rows; the routed call plans on
     the device and launches its grids for the caps (cap_experts = E, cap_rows = T k)."""
     D, I, fmt, E = cfg["D"], cfg["I"], cfg["fmt"], cfg["E"]
     i32 = dict(dtype=torch.int32, device="cuda")
@@ -394,22 +395,29 @@ def routed_prefill(np, torch, mvllm_hip, w, pool, cfg, T, steps, warmup):
                                 prepared=pool.lists[s % pool.layers])
 
     rec = {}
-    for key, fn in (("routed_dev_us", routed), ("host_planned_us", planned)):
-        for s in range(warmup):
-            fn(s)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for s in range(steps):
-            fn(s)
-        e1.record()
-        torch.cuda.synchronize()
-        rec[key] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
-    if int(status.cpu()[0]) != 0:
-        raise SystemExit("routed_dev reported status %d" % int(status.cpu()[0]))
-    rec["ratio"] = round(rec["routed_dev_us"] / rec["host_planned_us"], 4)
-    log(f"c4 device-resident block: {rec['routed_dev_us']:.1f} us per call, host-planned "
-        f"{rec['host_planned_us']:.1f} us ({rec['ratio']:.3f})")
+    for sfx, fp4 in (("", 0), ("_fp4act", 1)):
+        if not mvllm_hip.set_option("fp4act", fp4):
+            raise SystemExit("set_option fp4act failed")
+        try:
+            for key, fn in (("routed_dev_us", routed), ("host_planned_us", planned)):
+                for s in range(warmup):
+                    fn(s)
+                torch.cuda.synchronize()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for s in range(steps):
+                    fn(s)
+                e1.record()
+                torch.cuda.synchronize()
+                rec[key + sfx] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
+        finally:
+            mvllm_hip.set_option("fp4act", 0)
+        if int(status.cpu()[0]) != 0:
+            raise SystemExit("routed_dev reported status %d" % int(status.cpu()[0]))
+        rec["ratio" + sfx] = round(rec["routed_dev_us" + sfx] / rec["host_planned_us" + sfx], 4)
+        log(f"c4 device-resident block{sfx}: {rec['routed_dev_us' + sfx]:.1f} us per call, "
+            f"host-planned {rec['host_planned_us' + sfx]:.1f} us ({rec['ratio' + sfx]:.3f})")
     return rec
 
 

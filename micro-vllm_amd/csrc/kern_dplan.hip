@@ -25,15 +25,18 @@ namespace mvllm_hip {
 
 constexpr int kPlanThreads = 1024;
 
+// smallest class of 16 * 2^c rows that holds n rows
 __device__ __forceinline__ int dplan_class(int n) {
-    return n <= 16 ? 0 : n <= 32 ? 1 : n <= 64 ? 2 : 3;
+    return n <= 16 ? 0 : n <= 32 ? 1 : n <= 64 ? 2 : n <= 128 ? 3 : 4;
 }
 
 // Items per class of a segment of n live rows, the host planner's rule (plan_gemm): full
 // blocks of bm rows in the top class, the remainder in the smallest class that holds it,
 // or with split64 a remainder of 33-64 rows as two items of the 32-row class.
-__device__ __forceinline__ void dplan_counts(const DPlanArgs &A, int n, int (&k)[4]) {
-    k[0] = k[1] = k[2] = k[3] = 0;
+__device__ __forceinline__ void dplan_counts(const DPlanArgs &A, int n, int (&k)[kGemmClasses]) {
+#pragma unroll
+    for (int c = 0; c < kGemmClasses; ++c)
+        k[c] = 0;
     k[A.top] = n / A.bm;
     const int rem = n % A.bm;
     if (rem && A.split64 && rem > 32 && rem <= 64)
@@ -70,8 +73,8 @@ __device__ __forceinline__ const char *dplan_segment(const Args &A, int i, int n
 }
 
 __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
-    __shared__ int part[kPlanThreads][4];
-    __shared__ int tot[4];
+    __shared__ int part[kPlanThreads][kGemmClasses];
+    __shared__ int tot[kGemmClasses];
     const int tid = threadIdx.x;
     const int nb = min(max(A.counts[0], 0), A.cap_e);
     const int nrows = min(max(A.counts[1], 0), A.cap_rows);
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
     // segments [s0, s1) of this thread, in order
     const int per = (nb + kPlanThreads - 1) / kPlanThreads;
     const int s0 = min(nb, tid * per), s1 = min(nb, s0 + per);
-    int cnt[4] = {0, 0, 0, 0};
+    int cnt[kGemmClasses] = {};
     for (int i = s0; i < s1; ++i) {
         int x0, n;
         const char *blob = dplan_segment(A, i, nrows, x0, n);
@@ -103,18 +106,18 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
             continue;
         for (int j = x0; j < x0 + n; ++j)
             A.row_ok[j] = 1;
-        int k[4];
+        int k[kGemmClasses];
         dplan_counts(A, n, k);
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < kGemmClasses; ++c)
             cnt[c] += k[c];
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < kGemmClasses; ++c)
         part[tid][c] = cnt[c];
     __syncthreads();
-    // exclusive scan over threads, one class per wave of the first four
-    if (tid < 4 * 64) {
+    // exclusive scan over threads, one class per wave of the first kGemmClasses
+    if (tid < kGemmClasses * 64) {
         const int c = tid >> 6, l = tid & 63;
         constexpr int kPer = kPlanThreads / 64;  // 16 consecutive threads per lane
         int run = 0;
@@ -137,9 +140,9 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
             tot[c] = incl;
     }
     __syncthreads();
-    int pos[4];
+    int pos[kGemmClasses];
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+    for (int c = 0; c < kGemmClasses; ++c)
         pos[c] = part[tid][c];
     for (int i = s0; i < s1; ++i) {
         const ExpertWork &w = A.ew[i];
@@ -149,7 +152,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
         // block by column block).  A run that would pass the class's capacity (inputs whose
         // segments overlap) is written as items alone: a run's tasks index all its items,
         // and those past the capacity are never written.
-        int k[4], idx[4] = {0, 0, 0, 0};
+        int k[kGemmClasses], idx[kGemmClasses] = {};
         dplan_counts(A, n, k);
         auto put = [&](int c, int r0, int nrow) {
             const bool fits = pos[c] - idx[c] + k[c] <= A.item_cap[c];
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(kPlanThreads) void k_dplan(DPlanArgs A) {
             }
         }
     }
-    if (tid < 4)
+    if (tid < kGemmClasses)
         A.n_items[tid] = min(tot[tid], A.item_cap[tid]);
 }
 

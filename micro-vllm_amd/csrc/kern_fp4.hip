@@ -41,6 +41,7 @@ struct F4Args {
     float *out;             // single: Y f32 [rcap][O]
     int nbn, K, O, rcap;
     int xcd;  // 1: tasks ordered per XCD (xcd_task)
+    const int *n_items_dev;  // non-null: item count in device memory (grid sized for a bound)
     int act;
     float act_a, act_b;
 };
@@ -74,7 +75,11 @@ __global__ __launch_bounds__(kF4Threads) void k_gemm_fp4(F4Args A) {
     constexpr int UN = NB % 2 ? 2 * NB : NB;
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    const int n_tasks = (int)gridDim.x;
+    const int n_tasks = A.n_items_dev
+                            ? __builtin_amdgcn_readfirstlane(*A.n_items_dev) * A.nbn
+                            : (int)gridDim.x;
+    if ((int)blockIdx.x >= n_tasks)
+        return;
     const int task = A.xcd ? xcd_task(blockIdx.x, n_tasks) : (int)blockIdx.x;
     // An expert's run of nblk items owns tasks [g0 nbn, (g0 + nblk) nbn); they go column
     // block by column block, its row blocks adjacent, so that the row blocks running side
@@ -366,12 +371,13 @@ static hipError_t launch_f4_t(const F4Args &a, int n_items, hipStream_t st) {
 hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *items,
                            int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,
                            float *out, int K, int O, int rcap, int act, float act_a, float act_b,
-                           hipStream_t st) {
+                           hipStream_t st, const int *n_items_dev) {
     if (n_items <= 0)
         return hipSuccess;
     if (K % 256 || O % (dual ? 128 : 256))
         return hipErrorInvalidValue;
     F4Args a{};
+    a.n_items_dev = n_items_dev;
     a.ew = ew;
     a.items = static_cast<const F4Item *>(items);
     a.acode = acode;

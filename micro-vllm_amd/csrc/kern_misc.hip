@@ -144,8 +144,11 @@ __device__ __forceinline__ float e2m1_value(uint32_t c) {
 __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const int *rows_map,
                                                         int n, int K, uint8_t *codes,
                                                         uint8_t *scales, __bf16 *planes,
-                                                        const uint8_t *pmask) {
+                                                        const uint8_t *pmask,
+                                                        const int *n_live, int src_rows) {
     const uint32_t nb = (uint32_t)(K / 32);
+    if (n_live)  // rows past the device count are left alone
+        n = min(n, max(__builtin_amdgcn_readfirstlane(*n_live), 0));
     const uint32_t total = (uint32_t)n * nb;  // blocks
     const uint32_t lane = threadIdx.x & 63, e8 = lane & 7;
     const uint32_t wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
@@ -160,10 +163,12 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
             const bool ok = bid < total;
             row[u] = ok ? bid / nb : 0;
             blk[u] = ok ? bid - row[u] * nb : 0;
-            const uint32_t src = rows_map ? (uint32_t)rows_map[row[u]] : row[u];
-            v[u] = ok ? *reinterpret_cast<const float4 *>(x + (size_t)src * K + blk[u] * 32 +
-                                                          4 * e8)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int srci = rows_map ? rows_map[row[u]] : (int)row[u];
+            const bool live = ok && (src_rows < 0 || (srci >= 0 && srci < src_rows));
+            const uint32_t src = live ? (uint32_t)srci : 0u;
+            v[u] = live ? *reinterpret_cast<const float4 *>(x + (size_t)src * K + blk[u] * 32 +
+                                                            4 * e8)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int u = 0; u < kQU; ++u) {
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(256) void k_quantize_mxfp4(const float *x, const in
 
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st, const int *rows_map, void *planes,
-                                 const uint8_t *pmask) {
+                                 const uint8_t *pmask, const int *n_live, int src_rows) {
     if (n <= 0 || K <= 0 || K % 32 || (size_t)n * (K / 32) >= (size_t(1) << 31) ||
         (reinterpret_cast<uintptr_t>(x) & 15))
         return hipErrorInvalidValue;
@@ -224,7 +229,7 @@ hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, u
     const size_t wgs = (waves + 3) / 4;
     const unsigned grid = (unsigned)(wgs < 4096 ? wgs : 4096);
     hipLaunchKernelGGL(k_quantize_mxfp4, dim3(grid), dim3(256), 0, st, x, rows_map, n, K, codes,
-                       scales, static_cast<__bf16 *>(planes), pmask);
+                       scales, static_cast<__bf16 *>(planes), pmask, n_live, src_rows);
     return hipGetLastError();
 }
 

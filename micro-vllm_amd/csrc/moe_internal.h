@@ -67,10 +67,13 @@ hipError_t launch_membench(int kind, const void *src, void *dst, size_t bytes, i
                            hipStream_t st);
 // MXFP4 activation quantization of n rows of K (row j = x row rows_map[j], or j); planes
 // (optional, 8-byte aligned): the quantized values as bf16 rows [n][K] as well, for the
-// rows j with pmask[j] != 0 (every row when pmask is null).
+// rows j with pmask[j] != 0 (every row when pmask is null).  n_live (device, optional):
+// rows j >= *n_live are left alone (a launch sized for a bound); src_rows >= 0: a source
+// row outside [0, src_rows) quantizes as a zero row.
 hipError_t launch_quantize_mxfp4(const float *x, int n, int K, uint8_t *codes, uint8_t *scales,
                                  hipStream_t st, const int *rows_map = nullptr,
-                                 void *planes = nullptr, const uint8_t *pmask = nullptr);
+                                 void *planes = nullptr, const uint8_t *pmask = nullptr,
+                                 const int *n_live = nullptr, int src_rows = -1);
 
 // Routing on the device (kern_route.hip): moe_topk per token, and the segments of one
 // batched moe_block call.  Bit-exact with the host versions.
@@ -253,10 +256,12 @@ constexpr int kGemmClasses = 5;
 // ~680 us, 32-row 347 -> ~270 us).
 constexpr int kFp4BfMaxMt = 2;
 size_t fp4_lds_bytes(int mt);
+// n_items_dev (optional): the item count in device memory, n_items the bound the grid
+// covers (workgroups past the count exit).
 hipError_t launch_gemm_fp4(bool dual, int mt, const ExpertWork *ew, const void *items,
                            int n_items, const uint8_t *acode, const uint8_t *ascale, float *hout,
                            float *out, int K, int O, int rcap, int act, float act_a, float act_b,
-                           hipStream_t st);
+                           hipStream_t st, const int *n_items_dev = nullptr);
 
 // ---- device-planned calls (kern_dplan.hip) ---------------------------------------
 
@@ -274,8 +279,8 @@ struct DPlanArgs {
     int split64;       // remainders of 33-64 rows as two items of the 32-row class
     ExpertWork *ew;    // [cap_e]
     int4 *items;       // class c at items + item_base[c] ({expert, r0, nrow, 0})
-    int item_base[4], item_cap[4];
-    int *n_items;      // [4]
+    int item_base[kGemmClasses], item_cap[kGemmClasses];
+    int *n_items;      // [kGemmClasses]
     unsigned char *row_ok;  // [cap_rows]
     int *err;          // 0; 1 = a class overflowed its capacity (the bounds exclude it),
                        // 2 = a blob address not 256-byte aligned (that expert skipped)

@@ -1822,7 +1822,7 @@ int routed_dec(Ctx &C, int D, int I, int fmt, const void *const *table, int n_ta
                float *out, int S, int act, float act_a, float act_b, int *status,
                hipStream_t st, const long long off6[6]) {
     const int terms = C.mode == 1 ? 3 : C.mode == 2 ? 1 : 2;
-    if (C.gemm == 1 || S > 16 || D > kDecMaxK || I > kDecMaxK)
+    if (C.gemm == 1 || S > 16 || D > kDecMaxK || I > kDecMaxK || (fmt == 7 && C.fp4act))
         return -1;
     for (int k = 0; k < 6; ++k)  // weights 16-byte aligned, scales 16 (int4) or 8 (MXFP4)
         if (off6[k] % ((k & 1) && fmt == 7 ? 8 : 16))
@@ -2267,18 +2267,27 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
                               status, st, off6);
     if (rd >= 0)
         return rd;
+    // blobs are 256-byte aligned (k_dplan skips others): the pieces are 16-byte aligned
+    // when their offsets are
+    bool w16 = true;
+    for (int k = 0; k < 6; k += 2)
+        w16 = w16 && off6[k] % 16 == 0;
+    // native MXFP4 activations (option fp4act), as the host-planned call runs them: the
+    // scaled-FP4 GEMM's classes of up to 256 rows (its 16-byte weight rows), the 16- and
+    // 32-row classes on bf16 copies of the quantized activations
+    const bool fp4 = fmt == 7 && C.fp4act && w16;
     // bf16 terms per activation: two (2^-17 relative, the decode accuracy) for calls of at
     // most 256 rows, one (the prefill arithmetic) above; mode 1 always two, mode 2 one
-    const int terms = C.mode == 1 ? 2 : C.mode == 2 ? 1 : (cap_rows <= 256 ? 2 : 1);
-    const int max_mt = gemm_max_mt(fmt, terms);
-    const int top = max_mt == 8 ? 3 : 2, bm = 16 * max_mt;
+    const int terms = fp4 ? 1 : C.mode == 1 ? 2 : C.mode == 2 ? 1 : (cap_rows <= 256 ? 2 : 1);
+    const int max_mt = fp4 ? kFp4MaxMt : gemm_max_mt(fmt, terms);
+    const int top = max_mt == 16 ? 4 : max_mt == 8 ? 3 : 2, bm = 16 * max_mt;
     // remainders of 33-64 rows as two 32-row items, as the host planner does (plan_gemm)
-    const bool split64 = terms == 1 && max_mt >= 4;
+    const bool split64 = !fp4 && terms == 1 && max_mt >= 4;
     // items per class at most: one remainder per expert of >= lo rows; the top class's
     // items (full blocks and remainders above bm / 2) hold >= lo[top] rows each; with
     // split64 the 32-row class holds up to two items per expert, >= 16 rows per item
-    static const int lo[4] = {1, 17, 33, 65};
-    int cap[4] = {0, 0, 0, 0}, base[4] = {0, 0, 0, 0}, n_it = 0;
+    static const int lo[kGemmClasses] = {1, 17, 33, 65, 129};
+    int cap[kGemmClasses] = {}, base[kGemmClasses] = {}, n_it = 0;
     for (int c = 0; c <= top; ++c) {
         if (cap_rows >= lo[c])
             cap[c] = c == top ? cap_rows / lo[c] : std::min(cap_experts, cap_rows / lo[c]);
@@ -2297,9 +2306,19 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     if (!order_after_previous(C, st))
         return 0;
     HIP_TRY(C.Rp.ensure(total));
-    HIP_TRY(C.Xp.ensure((size_t)terms * cap_rows * D * 2));
-    HIP_TRY(C.Ph.ensure((size_t)terms * cap_rows * Iinter * 2));
-    HIP_TRY(C.Y.ensure((size_t)cap_rows * D * 4));
+    const size_t R = (size_t)cap_rows;
+    const bool bf = fp4 && (cap[0] || cap[1]);  // bf16 copies for the 16- and 32-row classes
+    if (fp4) {
+        HIP_TRY(C.Xp.ensure(R * (D / 2 + D / 32)));           // x codes + scales
+        HIP_TRY(C.Ph.ensure(R * (Iinter / 2 + Iinter / 32)));  // H codes + scales
+        HIP_TRY(C.H.ensure(R * Iinter * 4));
+        if (bf)
+            HIP_TRY(C.HP.ensure(R * (D + Iinter) * 2));
+    } else {
+        HIP_TRY(C.Xp.ensure((size_t)terms * R * D * 2));
+        HIP_TRY(C.Ph.ensure((size_t)terms * R * Iinter * 2));
+    }
+    HIP_TRY(C.Y.ensure(R * D * 4));
     char *p = static_cast<char *>(C.Rp.p);
     DPlanArgs a{};
     a.table = table;
@@ -2317,7 +2336,7 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     a.split64 = split64 ? 1 : 0;
     a.ew = reinterpret_cast<ExpertWork *>(p);
     a.items = reinterpret_cast<int4 *>(p + b_ew);
-    for (int c = 0; c < 4; ++c) {
+    for (int c = 0; c < kGemmClasses; ++c) {
         a.item_base[c] = base[c];
         a.item_cap[c] = cap[c];
     }
@@ -2337,26 +2356,60 @@ int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const
     cs.ent_row = reinterpret_cast<int *>(misc + b_misc + b_ok + b_cnt + b_cur);
     cs.ent_w = reinterpret_cast<float *>(misc + b_misc + b_ok + b_cnt + b_cur + b_er);
     HIP_TRY(launch_dplan(a, st));
-    HIP_TRY(launch_prep_planes(fmt, terms, x, rows, cap_rows, D, cap_rows, C.Xp.p, st,
-                               counts + 1, S));
-    // blobs are 256-byte aligned (k_dplan skips others): the pieces are 16-byte aligned
-    // when their offsets are
-    bool w16 = true;
-    for (int k = 0; k < 6; k += 2)
-        w16 = w16 && off6[k] % 16 == 0;
-    for (int c = 0; c <= top; ++c)
-        if (cap[c])
-            HIP_TRY(launch_gemm_cls(w16, fmt, true, terms, 1 << c, a.ew, a.items + base[c], cap[c],
-                                    C.Xp.p, C.Ph.p, nullptr, D, Iinter, cap_rows, act, act_a,
-                                    act_b, st, a.n_items + c));
-    for (int c = 0; c <= top; ++c)
-        if (cap[c])
-            HIP_TRY(launch_gemm_cls(w16, fmt, false, terms, 1 << c, a.ew, a.items + base[c],
-                                    cap[c], C.Ph.p, nullptr, static_cast<float *>(C.Y.p), Iinter,
-                                    D, cap_rows, 0, 0.f, 0.f, st, a.n_items + c));
+    float *Y = static_cast<float *>(C.Y.p);
+    if (fp4) {
+        // x rows quantized (gathered through rows; rows past the device count untouched,
+        // out-of-range tokens as zero rows), gate/up into H f32, H quantized, down into Y
+        uint8_t *xq = static_cast<uint8_t *>(C.Xp.p), *xsc = xq + R * (D / 2);
+        uint8_t *hq = static_cast<uint8_t *>(C.Ph.p), *hsc = hq + R * (Iinter / 2);
+        float *Hf = static_cast<float *>(C.H.p);
+        __bf16 *xb = bf ? static_cast<__bf16 *>(C.HP.p) : nullptr;
+        __bf16 *hb = bf ? xb + R * (size_t)D : nullptr;
+        HIP_TRY(launch_quantize_mxfp4(x, cap_rows, D, xq, xsc, st, rows, xb, nullptr,
+                                      counts + 1, S));
+        for (int c = 0; c <= top; ++c) {
+            if (!cap[c])
+                continue;
+            if ((1 << c) <= kFp4BfMaxMt)
+                HIP_TRY(launch_gemm(fmt, true, 1, 1 << c, a.ew, a.items + base[c], cap[c], xb,
+                                    nullptr, Hf, D, Iinter, cap_rows, act, act_a, act_b, st,
+                                    a.n_items + c));
+            else
+                HIP_TRY(launch_gemm_fp4(true, 1 << c, a.ew, a.items + base[c], cap[c], xq, xsc,
+                                        Hf, nullptr, D, Iinter, cap_rows, act, act_a, act_b, st,
+                                        a.n_items + c));
+        }
+        HIP_TRY(launch_quantize_mxfp4(Hf, cap_rows, Iinter, hq, hsc, st, nullptr, hb, nullptr,
+                                      counts + 1));
+        for (int c = 0; c <= top; ++c) {
+            if (!cap[c])
+                continue;
+            if ((1 << c) <= kFp4BfMaxMt)
+                HIP_TRY(launch_gemm(fmt, false, 1, 1 << c, a.ew, a.items + base[c], cap[c], hb,
+                                    nullptr, Y, Iinter, D, cap_rows, 0, 0.f, 0.f, st,
+                                    a.n_items + c));
+            else
+                HIP_TRY(launch_gemm_fp4(false, 1 << c, a.ew, a.items + base[c], cap[c], hq, hsc,
+                                        nullptr, Y, Iinter, D, cap_rows, 0, 0.f, 0.f, st,
+                                        a.n_items + c));
+        }
+    } else {
+        HIP_TRY(launch_prep_planes(fmt, terms, x, rows, cap_rows, D, cap_rows, C.Xp.p, st,
+                                   counts + 1, S));
+        for (int c = 0; c <= top; ++c)
+            if (cap[c])
+                HIP_TRY(launch_gemm_cls(w16, fmt, true, terms, 1 << c, a.ew, a.items + base[c],
+                                        cap[c], C.Xp.p, C.Ph.p, nullptr, D, Iinter, cap_rows, act,
+                                        act_a, act_b, st, a.n_items + c));
+        for (int c = 0; c <= top; ++c)
+            if (cap[c])
+                HIP_TRY(launch_gemm_cls(w16, fmt, false, terms, 1 << c, a.ew, a.items + base[c],
+                                        cap[c], C.Ph.p, nullptr, Y, Iinter, D, cap_rows, 0, 0.f,
+                                        0.f, st, a.n_items + c));
+    }
     HIP_TRY(launch_dcsr(cs, st));
     CombineArgs cb{};
-    cb.Y = static_cast<const float *>(C.Y.p);
+    cb.Y = Y;
     cb.tok_ptr = cs.cnt;
     cb.ent_row = cs.ent_row;
     cb.ent_w = cs.ent_w;

@@ -281,3 +281,95 @@ def test_routed_decode_surplus_caps(hip):
     finally:
         set_options(hip, combine_ordered=0, dec_ks=0)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def _fp4_bar(got, exp):
+    """Native-FP4 arithmetic against the composed oracle: exact e2m1 products, sums in
+    another order, so an h value may land across an e2m1 rounding boundary now and then
+    (the bar of the host-planned native-FP4 tests)."""
+    den = np.max(np.abs(exp))
+    rel = np.abs(got.astype(np.float64) - exp) / den
+    say("  rel_err max", float(rel.max()), "p99", float(np.quantile(rel, 0.99)))
+    assert float(rel.max()) < 1e-2
+    assert float(np.quantile(rel, 0.99)) < 1e-5
+
+
+def _oracle_fp4(orc, fmt, D, I, pool, geom, info, X, T, act, a, b, gone=()):
+    from mvllm_hip import synth
+    nb, eids, xoff, nr, rows, rw = info
+    lists = [[], [], [], [], [], []]
+    for e in eids:
+        pieces = synth.blob_pieces(pool[int(e)].cpu().numpy(), fmt, D, I, geom[1]) \
+            if int(e) not in gone else [None] * 6
+        for j in range(6):
+            lists[j].append(pieces[j])
+    exp = np.zeros((T, D), np.float32)
+    xg = X[np.clip(rows, 0, T - 1)]
+    assert orc.moe_block_fp4act(nb, D, I, fmt, *lists, xg, xoff, nr, rows, rw, exp, T, act,
+                                a, b) == 1
+    return exp
+
+
+@pytest.mark.parametrize("T,E,k,routing", [(6, 48, 4, "uniform"), (300, 64, 8, "skewed"),
+                                           (700, 32, 4, "skewed")])
+def test_routed_block_fp4act(hip, orc, T, E, k, routing):
+    """Option fp4act on the device-resident block: every call size takes the native-MXFP4
+    grouped path as the host-planned call does (x and H quantized to MXFP4, the scaled-FP4
+    GEMM for blocks of 33-256 rows, bf16 copies of the quantized values for the 16- and
+    32-row classes).  Bit for bit against the host-planned call on the same segments, and
+    within the native-FP4 bar of the composed oracle (orc_moe_block_fp4act)."""
+    from mvllm_hip import ACT_SITU
+    fmt, D, I = 7, 1024, 512
+    say("routed block fp4act", T, E, k, routing)
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 31 + T,
+                                                          routing=routing)
+    seg = route(hip, choice, mix, k)
+    set_options(hip, fp4act=1)
+    try:
+        got, status = run_routed(hip, fmt, D, I, table, seg, X, T, ACT_SITU, 4.0, 25.0)
+        ref, info = host_planned(hip, fmt, D, I, pool, stride, geom, seg, X, T, ACT_SITU, 4.0,
+                                 25.0, table)
+    finally:
+        set_options(hip, fp4act=0)
+    assert status == 0
+    say(f"  segments {info[0]}, rows {int(info[3].sum())}, largest {int(info[3].max())}")
+    if routing == "skewed":
+        assert int(info[3].max()) > 64  # the scaled-FP4 classes run
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    _fp4_bar(got, _oracle_fp4(orc, fmt, D, I, pool, geom, info, X, T, ACT_SITU, 4.0, 25.0))
+
+
+def test_routed_block_fp4act_dead_rows(hip, orc):
+    """Hand-made segments under fp4act: rows whose out row is out of range (quantized as
+    zero rows, never combined), a null expert and one outside the table (their rows
+    consumed without writing), a segment of 300 rows (a full 256-row block and a
+    remainder); caps above the sizes."""
+    from mvllm_hip import ACT_SITU
+    fmt, D, I, S, E = 7, 512, 256, 24, 16
+    rng, pool, stride, geom, X, _, _, table = layer(hip, fmt, D, I, S, E, 2, 808,
+                                                    null_ids=(5,))
+    eids = np.array([3, 5, 40, 11, 2], np.int32)  # 5: null; 40: outside the table
+    nr = np.array([300, 20, 7, 40, 3], np.int32)
+    xoff = np.concatenate([[0], np.cumsum(nr)[:-1]]).astype(np.int32)
+    n = int(nr.sum())
+    rows = rng.integers(0, S, n).astype(np.int32)
+    rows[[2, 50, 333, 360]] = [-1, S, -7, S + 3]
+    rw = rng.uniform(0.1, 1.0, n).astype(np.float32)
+    i32 = dict(dtype=torch.int32, device="cuda")
+    pad = 64  # caps above the sizes
+    seg = (torch.tensor([len(eids), n], **i32),
+           dev(np.concatenate([eids, np.zeros(pad, np.int32)])),
+           dev(np.concatenate([xoff, np.zeros(pad, np.int32)])),
+           dev(np.concatenate([nr, np.zeros(pad, np.int32)])),
+           dev(np.concatenate([rows, np.zeros(pad, np.int32)])),
+           dev(np.concatenate([rw, np.zeros(pad, np.float32)])))
+    set_options(hip, fp4act=1)
+    try:
+        got, status = run_routed(hip, fmt, D, I, table, seg, X, S, ACT_SITU, 4.0, 25.0)
+    finally:
+        set_options(hip, fp4act=0)
+    assert status == 0
+    info = (len(eids), eids, xoff, nr, rows, rw)
+    exp = _oracle_fp4(orc, fmt, D, I, pool, geom, info, X, S, ACT_SITU, 4.0, 25.0,
+                      gone=(5, 40))
+    _fp4_bar(got, exp)
