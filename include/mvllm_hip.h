@@ -214,8 +214,10 @@ int mvllm_hip_moe_route_dev(const float *choice, const float *mix, int n_tok, in
  * With option fp4act, MXFP4 experts (fmt 7) take the native-MXFP4 grouped path at every
  * size, as mvllm_hip_moe_block_dev does (x and H quantized as fp4_activation_qdq; blocks
  * of up to 256 rows; the same results as that call on the same segments).
- * fmt 4 / 7, D and Iinter multiples of 256, 1 <= S <= 65535.  status (device int, may be NULL) receives 0, or 2
- * when a blob address was not 256-byte aligned.  Enqueued on `stream`; 1 enqueued. */
+ * fmt 4 / 7, D and Iinter multiples of 256, 1 <= S <= 65535.  status (device int, may be
+ * NULL) receives 0; 2 when a blob address was not 256-byte aligned (that expert skipped);
+ * 1 when segments whose rows overlap made more work items than the caps bound (the
+ * surplus dropped; routing output never does).  Enqueued on `stream`; 1 enqueued. */
 int mvllm_hip_moe_block_routed_dev(int D, int Iinter, int fmt, const void *const *table,
                                    int n_table, const int *counts, const int *eids,
                                    const int *xoff, const int *nr, int cap_experts,

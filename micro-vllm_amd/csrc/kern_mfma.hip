@@ -83,7 +83,9 @@ __device__ __forceinline__ void seg_plan(const DecSegArgs &G, int item, int wg, 
         const bool any_err = __builtin_amdgcn_ballot_w64(err != 0) != 0;
         if (lane == 0) {
             *G.n_items = min(base, G.cap_items);
-            *G.err = any_err ? 2 : 0;
+            // 1: more items than the capacity (segments whose rows overlap; the items past
+            // it are dropped), as the planner kernel reports it
+            *G.err = any_err ? 2 : base > G.cap_items ? 1 : 0;
         }
     }
     if (__builtin_amdgcn_ballot_w64(mine) == 0 || item >= G.cap_items) {
