@@ -373,3 +373,38 @@ def test_routed_block_fp4act_dead_rows(hip, orc):
     exp = _oracle_fp4(orc, fmt, D, I, pool, geom, info, X, S, ACT_SITU, 4.0, 25.0,
                       gone=(5, 40))
     _fp4_bar(got, exp)
+
+
+@pytest.mark.parametrize("fmt,E", [(7, 256), (4, 160)])
+def test_routed_decode_self_planned(hip, orc, fmt, E):
+    """The default decode path, whose gate/up kernel finds its own item among the segments
+    (64 segments per scan step): a call of 16 tokens over more than 64 routed experts (two
+    or more scan steps), against the ordered path (the planner kernel's descriptors) within
+    the float-atomic combine's bar, against the oracle chain, and with caps above the
+    routed sizes (surplus workgroups find no item)."""
+    from mvllm_hip import ACT_CLAMP_SWIGLU, ACT_SITU
+    D, I, T, k = 1024, 512, 16, 8
+    act, a, b = (ACT_CLAMP_SWIGLU, 7.0, 0.0) if fmt == 4 else (ACT_SITU, 4.0, 25.0)
+    rng, pool, stride, geom, X, choice, mix, table = layer(hip, fmt, D, I, T, E, k, 61 + E)
+    seg = route(hip, choice, mix, k)
+    nb = int(seg[0].cpu().numpy()[0])
+    say(f"self-planned decode: fmt {fmt}, {nb} segments")
+    assert nb > 64
+    got, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)
+    assert status == 0
+    set_options(hip, combine_ordered=1)
+    try:
+        ordered, status = run_routed(hip, fmt, D, I, table, seg, X, T, act, a, b)
+    finally:
+        set_options(hip, combine_ordered=0)
+    assert status == 0
+    say("  vs ordered: rel", npref.rel_err(got, ordered))
+    assert npref.rel_err(got, ordered) < 1e-5
+    exp = oracle_chain(orc, fmt, D, I, pool, stride, geom, choice, mix, k, X, T, act, a, b)
+    say("  vs oracle chain: rel", npref.rel_err(got, exp))
+    assert npref.rel_err(got, exp) < 2e-5
+    big = route(hip, choice, mix, k, cap_rows=T * k + 300, cap_e=E + 40)
+    got2, status = run_routed(hip, fmt, D, I, table, big, X, T, act, a, b)
+    assert status == 0
+    say("  surplus caps vs exact: rel", npref.rel_err(got2, got))
+    assert npref.rel_err(got2, got) < 1e-6
