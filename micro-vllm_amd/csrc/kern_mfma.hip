@@ -41,13 +41,63 @@ void k_mfma_dec_inl(DecArgs A, DecInline I) {
 // item count and the status.
 __device__ __forceinline__ void seg_plan(const DecSegArgs &G, int item, int wg, int lane,
                                          DecDescK *kd) {
+    // the first 64 segments' fields loaded with the counts, before they are known
+    int e_l = -1, x_l = 0, nr_l = 0;
+    if (lane < G.cap_e) {
+        e_l = G.eids[lane];
+        x_l = G.xoff[lane];
+        nr_l = G.nr[lane];
+    }
     const int nb = min(max(G.counts[0], 0), G.cap_e);
     const int nrows = min(max(G.counts[1], 0), G.cap_rows);
     int base = 0, err = 0;
     bool mine = false;
     const char *my_blob = nullptr;
     int my_x0 = 0, my_n = 0, my_r0 = 0;
-    for (int c0 = 0; c0 < nb; c0 += 64) {  // uniform trip count
+    // Up to 64 segments (one lane each): the item's owner is found on the assumption that
+    // every segment with rows has a usable blob, and its rows are read together with the
+    // blob table; the general scan below runs only if some blob is not usable.
+    bool fast = nb <= 64;
+    int sp_rows[16];
+    float sp_w[16];
+    if (fast) {
+        const bool in = lane < nb;
+        const int n = !in || x_l < 0 || x_l > nrows ? 0 : max(0, min(nr_l, nrows - max(x_l, 0)));
+        const int cnt = n ? (n + G.rmax - 1) / G.rmax : 0;
+        int incl = cnt;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int v = __shfl_up(incl, o);
+            if (lane >= o)
+                incl += v;
+        }
+        const int excl = incl - cnt;
+        const bool own = cnt && item >= excl && item < incl;
+        const char *blob =
+            in && e_l >= 0 && e_l < G.n_table ? static_cast<const char *>(G.table[e_l]) : nullptr;
+        if (own) {
+            const int r0 = (item - excl) * G.rmax, jb = x_l + r0, nrow = min(G.rmax, n - r0);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                sp_rows[r] = r < nrow ? G.rows[jb + r] : 0;
+                sp_w[r] = r < nrow ? G.rw[jb + r] : 0.f;
+            }
+            my_x0 = x_l;
+            my_n = n;
+            my_r0 = r0;
+        }
+        const bool bad = n && (!blob || (reinterpret_cast<uintptr_t>(blob) & 255));
+        err = in && (reinterpret_cast<uintptr_t>(blob) & 255) ? 2 : 0;
+        if (__builtin_amdgcn_ballot_w64(bad) == 0) {
+            mine = own;
+            my_blob = blob;
+            base = __shfl(incl, 63);
+        } else {
+            fast = false;  // the general scan, with the blobs' validity
+            err = 0;
+            my_x0 = my_n = my_r0 = 0;
+        }
+    }
+    for (int c0 = 0; !fast && c0 < nb; c0 += 64) {  // uniform trip count
         const int i = c0 + lane;
         int cnt = 0, x0 = 0, n = 0;
         const char *blob = nullptr;
@@ -96,6 +146,13 @@ __device__ __forceinline__ void seg_plan(const DecSegArgs &G, int item, int wg, 
     if (!mine)
         return;
     const int jb = my_x0 + my_r0, nrow = min(G.rmax, my_n - my_r0);
+    if (!fast) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sp_rows[r] = r < nrow ? G.rows[jb + r] : 0;
+            sp_w[r] = r < nrow ? G.rw[jb + r] : 0.f;
+        }
+    }
     DecDescK k;
     k.w0 = my_blob + G.off[0];
     k.off[0] = (int)(G.off[2] - G.off[0]);
@@ -110,11 +167,11 @@ __device__ __forceinline__ void seg_plan(const DecSegArgs &G, int item, int wg, 
     d.nrow = nrow;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const int t = r < nrow ? G.rows[jb + r] : 0;
+        const int t = sp_rows[r];
         const bool ok = r < nrow && t >= 0 && t < G.S;
         k.rows[r] = (unsigned short)(ok ? t : 0);
         d.rows[r] = ok ? t : -1;
-        d.wts[r] = r < nrow ? G.rw[jb + r] : 0.f;
+        d.wts[r] = r < nrow ? sp_w[r] : 0.f;
     }
     *kd = k;
     if (wg == 0)
